@@ -1,0 +1,1020 @@
+// C ABI of the pocketinfer MI355X backend: the OpenClBackend twin
+// (backend/opencl.rs), explicit upload, test hooks and the device-resident
+// engine (model.rs:678-1352).  Host code only; kernels are in pi_kernels.hip.
+#include <hip/hip_runtime_api.h>
+
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "pi_common.h"
+#include "pi_detmath.h"
+#include "pi_kernels.h"
+
+struct pi_tensor {
+    pi_layout L;
+    uint8_t *dev = nullptr;
+};
+
+namespace {
+
+constexpr int kGemvMaxBlocks = 1024;   // persistent GEMV grid cap (4096 wavefronts)
+constexpr uint32_t kMaxBatch = 64;     // model.rs:12
+constexpr uint32_t kDecodeChunk = 16;  // decode steps launched between host checks
+
+struct Layer {
+    pi_tensor *q = nullptr, *k = nullptr, *v = nullptr, *o = nullptr;
+    pi_tensor *gate = nullptr, *up = nullptr, *down = nullptr;
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+
+struct Engine {
+    uint32_t n_layer = 0, n_embd = 0, n_ff = 0, n_head = 0, n_kv = 0, dh = 0, n_rot = 0, n_vocab = 0;
+    float eps = 1e-5f, theta = 10000.f;
+    uint32_t n_ctx = 0, nchunk = 0;
+    std::vector<uint32_t> eos;
+    std::vector<Layer> layers;
+    uint8_t *embd = nullptr;
+    uint32_t embd_type = 0;
+    uint64_t embd_row_bytes = 0;
+    pi_tensor *head = nullptr;
+    float *out_norm = nullptr;
+    float *kc = nullptr, *vc = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gate = nullptr,
+          *up = nullptr, *logits = nullptr, *scores = nullptr, *amax_v = nullptr;
+    uint32_t *amax_i = nullptr, *ids = nullptr, *prompt = nullptr;
+    int8_t *q8q = nullptr;
+    float *q8d = nullptr;
+    int32_t *q8s = nullptr;
+    pi_state *st = nullptr;
+    // graphs: layers in the batch-1 (NEON) and batch>1 (scalar) orders, logits,
+    // decode step, prefill step, and the last prompt token of a multi-token chunk
+    hipGraphExec_t g_layers_neon = nullptr, g_layers_seq = nullptr, g_logits = nullptr, g_decode = nullptr,
+                   g_prefill = nullptr, g_last_seq = nullptr;
+    std::vector<uint32_t> kv_tokens;
+    size_t cached_prefill_len = 0;
+    double last_decode_us = 0.0;
+};
+
+}  // namespace
+
+struct pi_ctx {
+    int device = 0;
+    hipStream_t own = nullptr, stream = nullptr;
+    std::string name, err;
+    bool fail_next = false;
+    bool use_graphs = true;   // replay captured graphs (else launch each kernel)
+    std::atomic<int> stop{0};
+    std::map<std::pair<uintptr_t, size_t>, pi_tensor *> wcache;
+    // grow-only IO buffers of matvec / test hooks (opencl.rs:461-482)
+    float *io_x = nullptr, *io_y = nullptr;
+    int8_t *io_q = nullptr;
+    float *io_d = nullptr;
+    int32_t *io_s = nullptr;
+    size_t cap_x = 0, cap_y = 0;
+    Engine *eng = nullptr;
+};
+
+namespace {
+
+int fail(pi_ctx *c, int code, const char *fmt, ...) {
+    if (c) {
+        char buf[512];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        c->err = buf;
+    }
+    return code;
+}
+
+#define HIPC(c, expr)                                                                          \
+    do {                                                                                       \
+        hipError_t e_ = (expr);                                                                \
+        if (e_ != hipSuccess) return fail((c), PI_E_HIP, "%s: %s", #expr, hipGetErrorString(e_)); \
+    } while (0)
+
+bool take_injected(pi_ctx *c) {
+    if (!c->fail_next) return false;
+    c->fail_next = false;
+    c->err = "injected failure";
+    return true;
+}
+
+template <typename T>
+int dalloc(pi_ctx *c, T **p, size_t n) {
+    *p = nullptr;
+    if (n == 0) n = 1;
+    hipError_t e = hipMalloc((void **)p, n * sizeof(T));
+    if (e != hipSuccess) return fail(c, PI_E_NOMEM, "hipMalloc(%zu bytes): %s", n * sizeof(T), hipGetErrorString(e));
+    return PI_OK;
+}
+
+void dfree(void *p) {
+    if (p) (void)hipFree(p);
+}
+
+int grow_io(pi_ctx *c, size_t k, size_t rows) {
+    if (k > c->cap_x) {
+        dfree(c->io_x); dfree(c->io_q); dfree(c->io_d); dfree(c->io_s);
+        c->io_x = nullptr; c->io_q = nullptr; c->io_d = nullptr; c->io_s = nullptr;
+        c->cap_x = 0;
+        int r;
+        if ((r = dalloc(c, &c->io_x, k)) || (r = dalloc(c, &c->io_q, k)) || (r = dalloc(c, &c->io_d, k / 32 + 1)) ||
+            (r = dalloc(c, &c->io_s, k / 32 + 1)))
+            return r;
+        c->cap_x = k;
+    }
+    if (rows > c->cap_y) {
+        dfree(c->io_y);
+        c->io_y = nullptr;
+        c->cap_y = 0;
+        int r = dalloc(c, &c->io_y, rows);
+        if (r) return r;
+        c->cap_y = rows;
+    }
+    return PI_OK;
+}
+
+// Upload native rows (host) and repack on the device.
+int upload_tensor(pi_ctx *c, uint32_t type, const void *host, size_t rows, size_t k, pi_tensor **out) {
+    *out = nullptr;
+    if (!pi_gemv_type(type)) return fail(c, PI_E_UNSUPPORTED, "tensor type %u has no HIP kernel", type);
+    if (!host || rows == 0 || rows > 0xFFFFFFFFu || k == 0 || k > 0xFFFFFFFFu)
+        return fail(c, PI_E_INVALID, "invalid upload arguments");
+    pi_layout L;
+    if (!pi_make_layout(type, (uint32_t)rows, (uint32_t)k, &L))
+        return fail(c, PI_E_INVALID, "row length %zu not supported for type %u", k, type);
+    size_t nbytes = pi_row_bytes(type, k) * rows;
+    uint8_t *staging = nullptr;
+    int r = dalloc(c, &staging, nbytes);
+    if (r) return r;
+    pi_tensor *t = new pi_tensor();
+    t->L = L;
+    r = dalloc(c, &t->dev, L.bytes);
+    if (r) { dfree(staging); delete t; return r; }
+    hipError_t e = hipMemcpyAsync(staging, host, nbytes, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemsetAsync(t->dev, 0, L.bytes, c->stream);
+    if (e == hipSuccess) e = pi_launch_repack(staging, t->dev, L, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    dfree(staging);
+    if (e != hipSuccess) {
+        dfree(t->dev);
+        delete t;
+        return fail(c, PI_E_HIP, "upload: %s", hipGetErrorString(e));
+    }
+    *out = t;
+    return PI_OK;
+}
+
+void free_tensor(pi_tensor *t) {
+    if (!t) return;
+    dfree(t->dev);
+    delete t;
+}
+
+// The self-test comparator: quant::dot_row as the reference evaluates it on
+// x86 for the two test blocks (quant.rs:377-441).  It only checks the GPU; it
+// is never used to produce results.
+float selftest_dot_q4k(const uint8_t *b, const float *x) {
+    float d = pi_f16_to_f32((uint16_t)(b[0] | (b[1] << 8))), dmin = pi_f16_to_f32((uint16_t)(b[2] | (b[3] << 8)));
+    const uint8_t *sc = b + 4, *qs = b + 16;
+    float tmp[256];
+    for (int is = 0; is < 8; is += 2) {
+        uint32_t s[2], m[2];
+        for (int t = 0; t < 2; t++) {
+            int j = is + t;
+            if (j < 4) { s[t] = sc[j] & 63u; m[t] = sc[j + 4] & 63u; }
+            else { s[t] = (sc[j + 4] & 0xFu) | ((sc[j - 4] >> 6) << 4); m[t] = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4); }
+        }
+        float d1 = d * (float)s[0], m1 = dmin * (float)m[0], d2 = d * (float)s[1], m2 = dmin * (float)m[1];
+        for (int l = 0; l < 32; l++) tmp[is * 32 + l] = d1 * (float)(qs[is / 2 * 32 + l] & 0xF) - m1;
+        for (int l = 0; l < 32; l++) tmp[is * 32 + 32 + l] = d2 * (float)(qs[is / 2 * 32 + l] >> 4) - m2;
+    }
+    float sum = 0.0f;
+    for (int j = 0; j < 256; j++) sum += tmp[j] * x[j];
+    return sum;
+}
+
+float selftest_dot_q6k(const uint8_t *b, const float *x) {
+    float d = pi_f16_to_f32((uint16_t)(b[208] | (b[209] << 8))), acc = 0.0f;
+    const uint8_t *ql = b, *qh = b + 128;
+    const int8_t *sc = (const int8_t *)(b + 192);
+    for (int half = 0; half < 2; half++)
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16, qlb = half * 64, qhb = half * 32, o = half * 128;
+            int q1 = (int)((ql[qlb + l] & 0xF) | (((qh[qhb + l] >> 0) & 3) << 4)) - 32;
+            int q2 = (int)((ql[qlb + l + 32] & 0xF) | (((qh[qhb + l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((ql[qlb + l] >> 4) | (((qh[qhb + l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((ql[qlb + l + 32] >> 4) | (((qh[qhb + l] >> 6) & 3) << 4)) - 32;
+            acc += d * (float)sc[half * 8 + is] * (float)q1 * x[o + l];
+            acc += d * (float)sc[half * 8 + is + 2] * (float)q2 * x[o + 32 + l];
+            acc += d * (float)sc[half * 8 + is + 4] * (float)q3 * x[o + 64 + l];
+            acc += d * (float)sc[half * 8 + is + 6] * (float)q4 * x[o + 96 + l];
+        }
+    return acc;
+}
+
+// ---------------------------------------------------------------------------
+// Engine
+// ---------------------------------------------------------------------------
+void engine_free(Engine *e) {
+    if (!e) return;
+    for (hipGraphExec_t g : {e->g_layers_neon, e->g_layers_seq, e->g_logits, e->g_decode, e->g_prefill, e->g_last_seq})
+        if (g) (void)hipGraphExecDestroy(g);
+    for (Layer &l : e->layers) {
+        for (pi_tensor *t : {l.q, l.k, l.v, l.o, l.gate, l.up, l.down}) free_tensor(t);
+        dfree(l.attn_norm);
+        dfree(l.ffn_norm);
+    }
+    free_tensor(e->head);
+    for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
+                    (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->attn,
+                    (void *)e->gate, (void *)e->up, (void *)e->logits, (void *)e->scores, (void *)e->amax_v,
+                    (void *)e->amax_i, (void *)e->ids, (void *)e->prompt, (void *)e->q8q, (void *)e->q8d,
+                    (void *)e->q8s, (void *)e->st})
+        dfree(p);
+    delete e;
+}
+
+bool check_shape(const pi_tensor_desc &t, uint64_t cols, uint64_t rows) { return t.ne0 == cols && t.ne1 == rows; }
+
+int upload_norm(pi_ctx *c, const pi_tensor_desc &t, uint32_t ne, float **out) {
+    if (t.type != PI_TYPE_F32) return fail(c, PI_E_UNSUPPORTED, "norm weights must be F32 (type %u)", t.type);
+    int r = dalloc(c, out, ne);
+    if (r) return r;
+    HIPC(c, hipMemcpy(*out, t.data, (size_t)ne * 4, hipMemcpyHostToDevice));
+    return PI_OK;
+}
+
+int upload_mat(pi_ctx *c, const pi_tensor_desc &t, pi_tensor **out) {
+    return upload_tensor(c, t.type, t.data, (size_t)t.ne1, (size_t)t.ne0, out);
+}
+
+// A grouped GEMV launch over matrices of one type and row length.
+pi_gemv_set make_set(std::initializer_list<std::pair<const pi_tensor *, float *>> mats) {
+    pi_gemv_set S{};
+    uint32_t t = 0, i = 0;
+    for (const auto &m : mats) {
+        S.w[i] = m.first->dev;
+        S.y[i] = m.second;
+        S.rows[i] = m.first->L.rows;
+        S.tile0[i] = t;
+        t += m.first->L.ntiles;
+        i++;
+    }
+    S.n = i;
+    for (; i < 4; i++) S.tile0[i] = t;
+    return S;
+}
+
+hipError_t gemv_set(const Engine &e, std::initializer_list<std::pair<const pi_tensor *, float *>> mats, int mode,
+                    hipStream_t s) {
+    const pi_gemv_set S = make_set(mats);
+    return pi_launch_gemv_group(S, mats.begin()->first->L, e.q8q, e.q8d, e.q8s, mode, kGemvMaxBlocks, s);
+}
+
+// Enqueues the layers of one token: state st holds (pos, tok).
+hipError_t enqueue_layers(const Engine &e, bool neon, hipStream_t s) {
+    hipError_t r;
+#define K(expr) do { if ((r = (expr)) != hipSuccess) return r; } while (0)
+    K(pi_launch_embed(e.embd, e.embd_type, e.n_embd, e.embd_row_bytes, e.st, e.x, s));
+    const float scale = 1.0f / sqrtf((float)e.dh);
+    for (uint32_t l = 0; l < e.n_layer; l++) {
+        const Layer &L = e.layers[l];
+        float *kc = e.kc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        float *vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        K(pi_launch_rmsnorm_q8(e.x, L.attn_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, neon, s));
+        if (L.v->L.type == L.q->L.type && L.k->L.type == L.q->L.type) {
+            K(gemv_set(e, {{L.q, e.q}, {L.k, e.k}, {L.v, e.v}}, PI_GEMV_OUT, s));
+        } else if (L.k->L.type == L.q->L.type) {
+            K(gemv_set(e, {{L.q, e.q}, {L.k, e.k}}, PI_GEMV_OUT, s));
+            K(gemv_set(e, {{L.v, e.v}}, PI_GEMV_OUT, s));
+        } else {
+            K(gemv_set(e, {{L.q, e.q}}, PI_GEMV_OUT, s));
+            K(gemv_set(e, {{L.k, e.k}}, PI_GEMV_OUT, s));
+            K(gemv_set(e, {{L.v, e.v}}, PI_GEMV_OUT, s));
+        }
+        K(pi_launch_rope_kv(e.q, e.k, e.v, e.cos_tab, e.sin_tab, e.st, kc, vc, e.n_head, e.n_kv, e.dh, e.n_rot / 2,
+                            e.n_ctx, s));
+        K(pi_launch_attention(e.q, kc, vc, e.st, e.n_head, e.n_kv, e.dh, e.n_ctx, scale, e.scores, e.nchunk, e.attn,
+                              e.q8q, e.q8d, e.q8s, neon, s));
+        K(gemv_set(e, {{L.o, e.x}}, PI_GEMV_RESIDUAL, s));
+        K(pi_launch_rmsnorm_q8(e.x, L.ffn_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, neon, s));
+        if (L.gate->L.type == L.up->L.type) {
+            K(gemv_set(e, {{L.gate, e.gate}, {L.up, e.up}}, PI_GEMV_OUT, s));
+        } else {
+            K(gemv_set(e, {{L.gate, e.gate}}, PI_GEMV_OUT, s));
+            K(gemv_set(e, {{L.up, e.up}}, PI_GEMV_OUT, s));
+        }
+        K(pi_launch_swiglu_q8(e.gate, e.up, e.n_ff, e.q8q, e.q8d, e.q8s, s));
+        K(gemv_set(e, {{L.down, e.x}}, PI_GEMV_RESIDUAL, s));
+    }
+    return hipSuccess;
+}
+
+hipError_t enqueue_logits(const Engine &e, hipStream_t s) {
+    hipError_t r;
+    // the head always normalizes one column: the batch-1 order (model.rs:1136-1143)
+    K(pi_launch_rmsnorm_q8(e.x, e.out_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, true, s));
+    K(gemv_set(e, {{e.head, e.logits}}, PI_GEMV_OUT, s));
+    return hipSuccess;
+}
+
+hipError_t enqueue_argmax(const Engine &e, uint32_t *ids, hipStream_t s) {
+    return pi_launch_argmax(e.logits, e.n_vocab, e.amax_v, e.amax_i, e.st, ids, s);
+}
+#undef K
+
+template <typename F>
+hipError_t capture(hipStream_t s, hipGraphExec_t *out, F enqueue) {
+    hipGraph_t g = nullptr;
+    hipError_t r = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (r != hipSuccess) return r;
+    hipError_t er = enqueue();
+    r = hipStreamEndCapture(s, &g);
+    if (er != hipSuccess) { if (g) (void)hipGraphDestroy(g); return er; }
+    if (r != hipSuccess) return r;
+    r = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    return r;
+}
+
+int build_graphs(pi_ctx *c, Engine &e) {
+    hipStream_t s = c->stream;
+    HIPC(c, capture(s, &e.g_layers_neon, [&] { return enqueue_layers(e, true, s); }));
+    HIPC(c, capture(s, &e.g_layers_seq, [&] { return enqueue_layers(e, false, s); }));
+    HIPC(c, capture(s, &e.g_logits, [&] { return enqueue_logits(e, s); }));
+    for (int neon = 0; neon < 2; neon++)
+        HIPC(c, capture(s, neon ? &e.g_decode : &e.g_last_seq, [&] {
+            hipError_t r = enqueue_layers(e, neon != 0, s);
+            if (r == hipSuccess) r = enqueue_logits(e, s);
+            if (r == hipSuccess) r = enqueue_argmax(e, e.ids, s);
+            return r;
+        }));
+    HIPC(c, capture(s, &e.g_prefill, [&] {
+        hipError_t r = enqueue_layers(e, false, s);
+        if (r == hipSuccess) r = pi_launch_advance(e.st, e.prompt, s);
+        return r;
+    }));
+    return PI_OK;
+}
+
+enum StepKind { STEP_LAYERS_NEON, STEP_LAYERS_SEQ, STEP_LOGITS, STEP_DECODE, STEP_PREFILL, STEP_LAST_SEQ };
+
+// One engine step on the context stream: a graph replay, or the same kernels
+// launched one by one when graphs are off (for tools that cannot follow
+// graph launches).
+hipError_t run_step(const pi_ctx *c, const Engine &e, StepKind k) {
+    hipStream_t s = c->stream;
+    if (c->use_graphs) {
+        const hipGraphExec_t g[] = {e.g_layers_neon, e.g_layers_seq, e.g_logits, e.g_decode, e.g_prefill, e.g_last_seq};
+        return hipGraphLaunch(g[k], s);
+    }
+    hipError_t r = hipSuccess;
+    switch (k) {
+    case STEP_LAYERS_NEON: return enqueue_layers(e, true, s);
+    case STEP_LAYERS_SEQ: return enqueue_layers(e, false, s);
+    case STEP_LOGITS: return enqueue_logits(e, s);
+    case STEP_PREFILL:
+        r = enqueue_layers(e, false, s);
+        return r == hipSuccess ? pi_launch_advance(e.st, e.prompt, s) : r;
+    case STEP_DECODE:
+    case STEP_LAST_SEQ:
+        r = enqueue_layers(e, k == STEP_DECODE, s);
+        if (r == hipSuccess) r = enqueue_logits(e, s);
+        return r == hipSuccess ? enqueue_argmax(e, e.ids, s) : r;
+    }
+    return hipErrorInvalidValue;
+}
+
+int set_state(pi_ctx *c, Engine &e, int32_t pos, uint32_t tok, uint32_t n_gen, uint32_t i) {
+    pi_state h{pos, tok, n_gen, i};
+    HIPC(c, hipMemcpyAsync(e.st, &h, sizeof h, hipMemcpyHostToDevice, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+extern "C" {
+
+int pi_hip_probe(char *buf, size_t n) {
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        if (buf && n) snprintf(buf, n, "no HIP device");
+        return PI_E_HIP;
+    }
+    for (int i = 0; i < count; i++) {
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, i) != hipSuccess) continue;
+        if (strncmp(p.gcnArchName, "gfx950", 6) == 0) {
+            if (buf && n) snprintf(buf, n, "%s (%s, %d CUs, %.0f GiB)", p.name, p.gcnArchName, p.multiProcessorCount,
+                                   (double)p.totalGlobalMem / (1024.0 * 1024.0 * 1024.0));
+            return PI_OK;
+        }
+    }
+    if (buf && n) snprintf(buf, n, "no gfx950 device among %d", count);
+    return PI_E_HIP;
+}
+
+int pi_hip_create(pi_ctx **out, int device) {
+    if (!out) return PI_E_INVALID;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) return PI_E_HIP;
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess) return PI_E_HIP;
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0) return PI_E_HIP;
+    if (hipSetDevice(device) != hipSuccess) return PI_E_HIP;
+    pi_ctx *c = new pi_ctx();
+    c->device = device;
+    if (hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking) != hipSuccess) {
+        delete c;
+        return PI_E_HIP;
+    }
+    c->stream = c->own;
+    char buf[300];
+    snprintf(buf, sizeof buf, "HIP %s (%s)", p.name, p.gcnArchName);
+    c->name = buf;
+    *out = c;
+    return PI_OK;
+}
+
+void pi_hip_destroy(pi_ctx *c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    engine_free(c->eng);
+    pi_hip_clear_weight_cache(c);
+    for (void *p : {(void *)c->io_x, (void *)c->io_y, (void *)c->io_q, (void *)c->io_d, (void *)c->io_s}) dfree(p);
+    if (c->own) (void)hipStreamDestroy(c->own);
+    delete c;
+}
+
+const char *pi_hip_name(const pi_ctx *c) { return c ? c->name.c_str() : ""; }
+const char *pi_last_error(const pi_ctx *c) { return c ? c->err.c_str() : "no context"; }
+
+int pi_hip_supports(const pi_ctx *c, uint32_t t) { return c && pi_gemv_type(t) ? 1 : 0; }
+
+void pi_hip_clear_weight_cache(pi_ctx *c) {
+    if (!c) return;
+    for (auto &kv : c->wcache) free_tensor(kv.second);
+    c->wcache.clear();
+}
+
+int pi_hip_set_stream(pi_ctx *c, void *s) {
+    if (!c) return PI_E_INVALID;
+    c->stream = s ? (hipStream_t)s : c->own;
+    return PI_OK;
+}
+
+int pi_hip_synchronize(pi_ctx *c) {
+    if (!c) return PI_E_INVALID;
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_use_graphs(pi_ctx *c, int enable) {
+    if (!c) return PI_E_INVALID;
+    c->use_graphs = enable != 0;
+    return PI_OK;
+}
+
+int pi_hip_fail_next(pi_ctx *c) {
+    if (!c) return PI_E_INVALID;
+    c->fail_next = true;
+    return PI_OK;
+}
+
+int pi_hip_upload(pi_ctx *c, uint32_t type, const void *host, size_t rows, size_t k, pi_tensor **out) {
+    if (!c || !out) return PI_E_INVALID;
+    return upload_tensor(c, type, host, rows, k, out);
+}
+
+void pi_hip_tensor_free(pi_ctx *c, pi_tensor *t) {
+    (void)c;
+    free_tensor(t);
+}
+
+size_t pi_hip_tensor_bytes(const pi_tensor *t) { return t ? (size_t)t->L.bytes : 0; }
+
+int pi_hip_gemv_q8_dev(pi_ctx *c, const pi_tensor *w, const int8_t *q, const float *d, const int32_t *s, float *y) {
+    if (!c || !w || !q || !d || !s || !y) return PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    HIPC(c, pi_launch_gemv(w->dev, w->L, q, d, s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+    return PI_OK;
+}
+
+int pi_hip_gemv_dev(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
+    if (!c || !w || !x || !y) return PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    int r = grow_io(c, w->L.k, 1);
+    if (r) return r;
+    HIPC(c, pi_launch_q8(x, w->L.k, 1, c->io_q, c->io_d, c->io_s, c->stream));
+    HIPC(c, pi_launch_gemv(w->dev, w->L, c->io_q, c->io_d, c->io_s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+    return PI_OK;
+}
+
+int pi_hip_q8_quantize_dev(pi_ctx *c, const float *x, size_t k, int b, int8_t *q, float *d, int32_t *s) {
+    if (!c || !x || !q || !d || !s || k == 0 || k % 32 || b < 1 || b > 64) return PI_E_INVALID;
+    HIPC(c, pi_launch_q8(x, (uint32_t)k, (uint32_t)b, q, d, s, c->stream));
+    return PI_OK;
+}
+
+int pi_hip_dev_alloc(pi_ctx *c, size_t bytes, void **out) {
+    if (!c || !out) return PI_E_INVALID;
+    *out = nullptr;
+    HIPC(c, hipSetDevice(c->device));
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(c, PI_E_NOMEM, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    return PI_OK;
+}
+
+void pi_hip_dev_free(pi_ctx *c, void *p) {
+    (void)c;
+    dfree(p);
+}
+
+int pi_hip_copy_h2d(pi_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (!c || !dst || !src) return PI_E_INVALID;
+    HIPC(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_copy_d2h(pi_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (!c || !dst || !src) return PI_E_INVALID;
+    HIPC(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_time_gemv(pi_ctx *c, const pi_tensor *const *ws, int n_copies, const int8_t *q, const float *d,
+                     const int32_t *s, float *y, int iters, double *avg_us) {
+    if (!c || !ws || n_copies < 1 || iters < 1 || !avg_us) return PI_E_INVALID;
+    hipEvent_t a, b;
+    HIPC(c, hipEventCreate(&a));
+    HIPC(c, hipEventCreate(&b));
+    HIPC(c, hipEventRecord(a, c->stream));
+    for (int i = 0; i < iters; i++) {
+        const pi_tensor *w = ws[i % n_copies];
+        HIPC(c, pi_launch_gemv(w->dev, w->L, q, d, s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+    }
+    HIPC(c, hipEventRecord(b, c->stream));
+    HIPC(c, hipEventSynchronize(b));
+    float ms = 0.f;
+    HIPC(c, hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *avg_us = (double)ms * 1000.0 / iters;
+    return PI_OK;
+}
+
+int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, size_t k, const float *x, float *out,
+                  size_t rows) {
+    if (!c || !w || !x || !out || rows == 0 || k == 0) return c ? fail(c, PI_E_INVALID, "invalid matvec arguments") : PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    if (!pi_gemv_type(type)) return fail(c, PI_E_UNSUPPORTED, "type not supported");
+    if (pi_row_bytes(type, k) * rows != w_bytes)
+        return fail(c, PI_E_INVALID, "weight bytes %zu do not match %zu rows of k=%zu", w_bytes, rows, k);
+    auto key = std::make_pair((uintptr_t)w, w_bytes);
+    pi_tensor *t;
+    auto it = c->wcache.find(key);
+    if (it != c->wcache.end() && it->second->L.k == k && it->second->L.type == type) {
+        t = it->second;
+    } else {
+        if (it != c->wcache.end()) { free_tensor(it->second); c->wcache.erase(it); }
+        int r = upload_tensor(c, type, w, rows, k, &t);
+        if (r) return r;
+        c->wcache[key] = t;
+    }
+    int r = grow_io(c, k, rows);
+    if (r) return r;
+    HIPC(c, hipMemcpyAsync(c->io_x, x, k * 4, hipMemcpyHostToDevice, c->stream));
+    HIPC(c, pi_launch_q8(c->io_x, (uint32_t)k, 1, c->io_q, c->io_d, c->io_s, c->stream));
+    HIPC(c, pi_launch_gemv(t->dev, t->L, c->io_q, c->io_d, c->io_s, c->io_y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks,
+                           c->stream));
+    HIPC(c, hipMemcpyAsync(out, c->io_y, rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_selftest(pi_ctx *c) {
+    if (!c) return PI_E_INVALID;
+    const size_t k = 256;
+    float x[256];
+    for (size_t j = 0; j < k; j++) x[j] = (float)(j % 7) * 0.1f - 0.3f;
+    uint8_t w4[144] = {0};
+    w4[0] = 0x00; w4[1] = 0x3C;  // d = 1.0
+    w4[4] = 1;
+    for (int i = 0; i < 128; i++) w4[16 + i] = 0x21;
+    float out4 = 0.f;
+    int r = pi_hip_matvec(c, PI_TYPE_Q4_K, w4, sizeof w4, k, x, &out4, 1);
+    if (r) { pi_hip_clear_weight_cache(c); return r; }
+    float want4 = selftest_dot_q4k(w4, x);
+    if (std::fabs(out4 - want4) > std::fabs(want4) * 0.02f + 0.01f) {
+        pi_hip_clear_weight_cache(c);
+        return fail(c, PI_E_SELFTEST, "q4_K self-test failed: gpu=%g cpu=%g", out4, want4);
+    }
+    uint8_t w6[210] = {0};
+    for (int i = 0; i < 128; i++) w6[i] = 0x95;
+    for (int i = 0; i < 64; i++) w6[128 + i] = 0x1B;
+    for (int i = 0; i < 16; i++) w6[192 + i] = 2;
+    w6[208] = 0x00; w6[209] = 0x3C;
+    float out6 = 0.f;
+    r = pi_hip_matvec(c, PI_TYPE_Q6_K, w6, sizeof w6, k, x, &out6, 1);
+    if (r) { pi_hip_clear_weight_cache(c); return r; }
+    float want6 = selftest_dot_q6k(w6, x);
+    if (std::fabs(out6 - want6) > std::fabs(want6) * 0.02f + 0.01f) {
+        pi_hip_clear_weight_cache(c);
+        return fail(c, PI_E_SELFTEST, "q6_K self-test failed: gpu=%g cpu=%g", out6, want6);
+    }
+    pi_hip_clear_weight_cache(c);
+    return PI_OK;
+}
+
+int pi_hip_q8_quantize(pi_ctx *c, const float *x, size_t k, int b, int8_t *q, float *d, int32_t *sum) {
+    if (!c || !x || !q || !d || !sum || k == 0 || k % 32 || b < 1 || b > 64) return PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    float *dx = nullptr;
+    int8_t *dq = nullptr;
+    float *dd = nullptr;
+    int32_t *ds = nullptr;
+    size_t n = k * (size_t)b, nb = k / 32 * (size_t)b;
+    int r;
+    if ((r = dalloc(c, &dx, n)) || (r = dalloc(c, &dq, n)) || (r = dalloc(c, &dd, nb)) || (r = dalloc(c, &ds, nb))) {
+        dfree(dx); dfree(dq); dfree(dd); dfree(ds);
+        return r;
+    }
+    hipError_t e = hipMemcpyAsync(dx, x, n * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = pi_launch_q8(dx, (uint32_t)k, (uint32_t)b, dq, dd, ds, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(q, dq, n, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(d, dd, nb * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(sum, ds, nb * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    dfree(dx); dfree(dq); dfree(dd); dfree(ds);
+    if (e != hipSuccess) return fail(c, PI_E_HIP, "q8_quantize: %s", hipGetErrorString(e));
+    return PI_OK;
+}
+
+int pi_hip_block_sums(pi_ctx *c, const pi_tensor *w, const int8_t *q, const float *d, const int32_t *sum,
+                      int32_t *sums) {
+    if (!c || !w || !q || !d || !sum || !sums) return PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    const size_t k = w->L.k, nb = k / 32;
+    const size_t per_row = (w->L.type == PI_TYPE_Q6_K) ? k / 16 : k / 32;
+    const size_t n = per_row * w->L.rows;
+    int32_t *dsums = nullptr;
+    int r = grow_io(c, k, 1);
+    if (r) return r;
+    if ((r = dalloc(c, &dsums, n))) return r;
+    hipError_t e = hipMemcpyAsync(c->io_q, q, k, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->io_d, d, nb * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(c->io_s, sum, nb * 4, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess)
+        e = pi_launch_gemv(w->dev, w->L, c->io_q, c->io_d, c->io_s, nullptr, dsums, PI_GEMV_SUMS, kGemvMaxBlocks, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(sums, dsums, n * 4, hipMemcpyDeviceToHost, c->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    dfree(dsums);
+    if (e != hipSuccess) return fail(c, PI_E_HIP, "block_sums: %s", hipGetErrorString(e));
+    return PI_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Engine entry points
+// ---------------------------------------------------------------------------
+int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
+    if (!c || !m || !m->layers || n_ctx == 0) return c ? fail(c, PI_E_INVALID, "invalid model descriptor") : PI_E_INVALID;
+    engine_free(c->eng);
+    c->eng = nullptr;
+    // Config::from_gguf / Model::finish checks (model.rs:43-81, 571-601)
+    if (m->n_layer == 0 || m->n_embd == 0 || m->n_ff == 0 || m->n_head == 0)
+        return fail(c, PI_E_INVALID, "invalid model configuration: zero layer, hidden, FFN or head count");
+    if (m->head_dim == 0 || m->n_head_kv == 0 || m->n_head % m->n_head_kv)
+        return fail(c, PI_E_INVALID, "invalid GQA configuration");
+    if (m->n_rot == 0 || m->n_rot > m->head_dim || m->n_rot % 2 || !std::isfinite(m->rope_theta) || m->rope_theta <= 0.f ||
+        !std::isfinite(m->rms_eps) || m->rms_eps <= 0.f)
+        return fail(c, PI_E_INVALID, "invalid RoPE / RMSNorm configuration");
+    if (m->head_dim != 64) return fail(c, PI_E_UNSUPPORTED, "attention kernel supports head_dim 64 (got %u)", m->head_dim);
+    if (m->n_embd % 32 || m->n_ff % 32) return fail(c, PI_E_UNSUPPORTED, "hidden and FFN sizes must be multiples of 32");
+    const uint64_t ne = m->n_embd, vocab = m->token_embd.ne1;
+    const uint64_t qdim = (uint64_t)m->n_head * m->head_dim, kdim = (uint64_t)m->n_head_kv * m->head_dim;
+    if (qdim != ne) return fail(c, PI_E_UNSUPPORTED, "n_head*head_dim must equal n_embd");
+    if (vocab == 0 || m->token_embd.ne0 != ne || (m->n_vocab && m->n_vocab != vocab))
+        return fail(c, PI_E_INVALID, "embedding / metadata / tokenizer vocab dimensions disagree");
+    if (!check_shape(m->output, ne, vocab) || !check_shape(m->output_norm, ne, 1))
+        return fail(c, PI_E_INVALID, "output tensor shape mismatch");
+    for (uint32_t l = 0; l < m->n_layer; l++) {
+        const pi_layer_desc &L = m->layers[l];
+        if (!check_shape(L.attn_norm, ne, 1) || !check_shape(L.ffn_norm, ne, 1) || !check_shape(L.attn_q, ne, qdim) ||
+            !check_shape(L.attn_k, ne, kdim) || !check_shape(L.attn_v, ne, kdim) || !check_shape(L.attn_o, qdim, ne) ||
+            !check_shape(L.ffn_gate, ne, m->n_ff) || !check_shape(L.ffn_up, ne, m->n_ff) ||
+            !check_shape(L.ffn_down, m->n_ff, ne))
+            return fail(c, PI_E_INVALID, "layer %u tensor shape mismatch", l);
+    }
+    if (pi_type_block_elems(m->token_embd.type) == 0)
+        return fail(c, PI_E_UNSUPPORTED, "token_embd type %u unsupported", m->token_embd.type);
+    Engine *e = new Engine();
+    e->n_layer = m->n_layer; e->n_embd = m->n_embd; e->n_ff = m->n_ff; e->n_head = m->n_head;
+    e->n_kv = m->n_head_kv; e->dh = m->head_dim; e->n_rot = m->n_rot; e->n_vocab = (uint32_t)vocab;
+    e->eps = m->rms_eps; e->theta = m->rope_theta; e->n_ctx = n_ctx;
+    e->nchunk = (n_ctx + 63) / 64;
+    e->eos.assign(m->eos_ids, m->eos_ids + m->n_eos);
+    e->layers.resize(m->n_layer);
+    int r = PI_OK;
+#define TRY(expr) do { if ((r = (expr)) != PI_OK) { engine_free(e); return r; } } while (0)
+    for (uint32_t l = 0; l < m->n_layer; l++) {
+        const pi_layer_desc &D = m->layers[l];
+        Layer &L = e->layers[l];
+        TRY(upload_mat(c, D.attn_q, &L.q));
+        TRY(upload_mat(c, D.attn_k, &L.k));
+        TRY(upload_mat(c, D.attn_v, &L.v));
+        TRY(upload_mat(c, D.attn_o, &L.o));
+        TRY(upload_mat(c, D.ffn_gate, &L.gate));
+        TRY(upload_mat(c, D.ffn_up, &L.up));
+        TRY(upload_mat(c, D.ffn_down, &L.down));
+        TRY(upload_norm(c, D.attn_norm, e->n_embd, &L.attn_norm));
+        TRY(upload_norm(c, D.ffn_norm, e->n_embd, &L.ffn_norm));
+    }
+    TRY(upload_mat(c, m->output, &e->head));
+    TRY(upload_norm(c, m->output_norm, e->n_embd, &e->out_norm));
+    e->embd_type = m->token_embd.type;
+    e->embd_row_bytes = pi_row_bytes(e->embd_type, ne);
+    if (e->embd_row_bytes == 0) { engine_free(e); return fail(c, PI_E_UNSUPPORTED, "token_embd row length"); }
+    TRY(dalloc(c, &e->embd, e->embd_row_bytes * vocab));
+    if (hipMemcpy(e->embd, m->token_embd.data, e->embd_row_bytes * vocab, hipMemcpyHostToDevice) != hipSuccess) {
+        engine_free(e);
+        return fail(c, PI_E_HIP, "token_embd upload failed");
+    }
+    // KV cache [layer][kv_head][n_ctx][head_dim] f32, zeroed (model.rs:362-373)
+    const uint64_t nkv = (uint64_t)e->n_layer * e->n_kv * n_ctx * e->dh;
+    TRY(dalloc(c, &e->kc, nkv));
+    TRY(dalloc(c, &e->vc, nkv));
+    if (hipMemset(e->kc, 0, nkv * 4) != hipSuccess || hipMemset(e->vc, 0, nkv * 4) != hipSuccess) {
+        engine_free(e);
+        return fail(c, PI_E_HIP, "KV clear failed");
+    }
+    // RoPE tables (model.rs:413-417, 445-460), host libm like the reference
+    const uint32_t half = e->n_rot / 2;
+    std::vector<float> inv(half), ct((size_t)n_ctx * half), stt((size_t)n_ctx * half);
+    for (uint32_t i = 0; i < half; i++) inv[i] = 1.0f / pi_powf(e->theta, 2.0f * (float)i / (float)e->n_rot);
+    for (uint32_t p = 0; p < n_ctx; p++)
+        for (uint32_t i = 0; i < half; i++) {
+            float a = (float)p * inv[i];
+            ct[(size_t)p * half + i] = pi_cosf(a);
+            stt[(size_t)p * half + i] = pi_sinf(a);
+        }
+    TRY(dalloc(c, &e->cos_tab, ct.size()));
+    TRY(dalloc(c, &e->sin_tab, stt.size()));
+    if (hipMemcpy(e->cos_tab, ct.data(), ct.size() * 4, hipMemcpyHostToDevice) != hipSuccess ||
+        hipMemcpy(e->sin_tab, stt.data(), stt.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+        engine_free(e);
+        return fail(c, PI_E_HIP, "RoPE table upload failed");
+    }
+    const uint32_t big = e->n_embd > e->n_ff ? e->n_embd : e->n_ff;
+    TRY(dalloc(c, &e->x, ne)); TRY(dalloc(c, &e->q, qdim)); TRY(dalloc(c, &e->k, kdim)); TRY(dalloc(c, &e->v, kdim));
+    TRY(dalloc(c, &e->attn, qdim)); TRY(dalloc(c, &e->gate, e->n_ff)); TRY(dalloc(c, &e->up, e->n_ff));
+    TRY(dalloc(c, &e->logits, vocab));
+    TRY(dalloc(c, &e->scores, (size_t)e->n_head * n_ctx));
+    TRY(dalloc(c, &e->amax_v, PI_ARGMAX_BLOCKS)); TRY(dalloc(c, &e->amax_i, PI_ARGMAX_BLOCKS));
+    TRY(dalloc(c, &e->ids, (size_t)n_ctx + kDecodeChunk + 2)); TRY(dalloc(c, &e->prompt, (size_t)n_ctx + 1));
+    TRY(dalloc(c, &e->q8q, big)); TRY(dalloc(c, &e->q8d, big / 32)); TRY(dalloc(c, &e->q8s, big / 32));
+    TRY(dalloc(c, &e->st, 1));
+    if (hipMemset(e->logits, 0, vocab * 4) != hipSuccess) { engine_free(e); return fail(c, PI_E_HIP, "memset"); }
+    TRY(build_graphs(c, *e));
+#undef TRY
+    c->eng = e;
+    return PI_OK;
+}
+
+static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int b, int want_logits, bool cancellable) {
+    Engine *e = c->eng;
+    if (b < 1 || (uint32_t)b > kMaxBatch) return fail(c, PI_E_INVALID, "invalid batch %d", b);
+    for (int i = 0; i < b; i++) {
+        if (pos[i] < 0 || (uint32_t)pos[i] >= e->n_ctx) return fail(c, PI_E_CONTEXT_FULL, "context full");
+        if (ids[i] >= e->n_vocab) return fail(c, PI_E_INVALID, "token %u out of vocab", ids[i]);
+        if (i > 0 && pos[i] <= pos[i - 1]) return fail(c, PI_E_INVALID, "batch positions must increase");
+    }
+    for (int i = 0; i < b; i++) {
+        if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
+        int r = set_state(c, *e, pos[i], ids[i], 0, 0);
+        if (r) return r;
+        // a batch of more than one token evaluates in the scalar order (model.rs:812-822, 1028-1038)
+        HIPC(c, run_step(c, *e, b > 1 ? STEP_LAYERS_SEQ : STEP_LAYERS_NEON));
+    }
+    if (want_logits) HIPC(c, run_step(c, *e, STEP_LOGITS));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_forward(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int b, int want_logits) {
+    if (!c) return PI_E_INVALID;
+    if (!c->eng) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (!ids || !pos) return fail(c, PI_E_INVALID, "null ids/positions");
+    if (take_injected(c)) return PI_E_INJECTED;
+    // Engine::forward invalidates reuse (model.rs:825-831)
+    c->eng->kv_tokens.clear();
+    c->eng->cached_prefill_len = 0;
+    return forward_impl(c, ids, pos, b, want_logits, false);
+}
+
+int pi_hip_logits(pi_ctx *c, float *out, size_t n) {
+    if (!c || !out) return PI_E_INVALID;
+    if (!c->eng) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (n > c->eng->n_vocab) return fail(c, PI_E_INVALID, "asked for %zu logits of %u", n, c->eng->n_vocab);
+    HIPC(c, hipMemcpyAsync(out, c->eng->logits, n * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_argmax(pi_ctx *c, uint32_t *id) {
+    if (!c || !id) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    HIPC(c, enqueue_argmax(*e, nullptr, c->stream));
+    pi_state h;
+    HIPC(c, hipMemcpyAsync(&h, e->st, sizeof h, hipMemcpyDeviceToHost, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    *id = h.tok;
+    return PI_OK;
+}
+
+void pi_hip_request_stop(pi_ctx *c) { if (c) c->stop.store(1); }
+void pi_hip_clear_stop(pi_ctx *c) { if (c) c->stop.store(0); }
+
+int pi_hip_last_decode_us(pi_ctx *c, double *us) {
+    if (!c || !us || !c->eng) return PI_E_INVALID;
+    *us = c->eng->last_decode_us;
+    return PI_OK;
+}
+
+int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopts *o, pi_genstats *st,
+                    uint32_t *gen_ids) {
+    if (!c || !o || !st) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    memset(st, 0, sizeof *st);
+    snprintf(st->stop, sizeof st->stop, "max_tokens");
+    if (n == 0 || !prompt) return fail(c, PI_E_INVALID, "empty prompt");
+    if (o->temp > 0.0f) return fail(c, PI_E_UNSUPPORTED, "only greedy decoding (temp <= 0) runs on the device");
+    if (o->max_tokens > 0 && !gen_ids) return fail(c, PI_E_INVALID, "gen_ids is null");
+    if (take_injected(c)) return PI_E_INJECTED;
+    for (size_t i = 0; i < n; i++)
+        if (prompt[i] >= e->n_vocab) return fail(c, PI_E_INVALID, "token %u out of vocab", prompt[i]);
+    if (n > e->n_ctx) return fail(c, PI_E_CONTEXT_FULL, "context full");
+    auto t0 = std::chrono::steady_clock::now();
+    const size_t chunk = 32;
+    // Reuse rule of model.rs:1258-1268.  The device prefill evaluates every
+    // token with the same kernels whatever the chunking, so full-chunk reuse
+    // is exact here and stays enabled while this backend is active.
+    size_t common = 0;
+    while (common < e->kv_tokens.size() && common < n && e->kv_tokens[common] == prompt[common]) common++;
+    size_t reused = std::min(std::min(common, e->cached_prefill_len), n - 1) / chunk * chunk;
+    e->kv_tokens.resize(reused);
+    e->cached_prefill_len = 0;
+    st->prefill_cached_tokens = (uint32_t)reused;
+    HIPC(c, hipMemcpyAsync(e->prompt, prompt, n * 4, hipMemcpyHostToDevice, c->stream));
+    int r = set_state(c, *e, (int32_t)reused, prompt[reused], 0, (uint32_t)reused);
+    if (r) return r;
+    size_t off = reused;
+    bool stopped = false;
+    // Prefill in 32-token chunks from `reused` (model.rs:1269-1288).  Tokens of
+    // a chunk of more than one token take the scalar-order graph; the last
+    // prompt token also computes logits and the first greedy id.
+    const size_t last_chunk = (n - reused) % chunk == 0 ? chunk : (n - reused) % chunk;
+    while (off + 1 < n) {
+        if (c->stop.load()) { stopped = true; break; }
+        size_t end = std::min(n - 1, off + chunk);
+        for (size_t t = off; t < end; t++) HIPC(c, run_step(c, *e, STEP_PREFILL));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        e->kv_tokens.insert(e->kv_tokens.end(), prompt + off, prompt + end);
+        off = end;
+    }
+    if (!stopped && c->stop.load()) stopped = true;
+    if (stopped) {
+        snprintf(st->stop, sizeof st->stop, "user_stop");
+        st->prefill_tokens = (uint32_t)(off - reused);
+        e->kv_tokens.clear();
+        st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+        return PI_OK;
+    }
+    HIPC(c, run_step(c, *e, last_chunk > 1 ? STEP_LAST_SEQ : STEP_DECODE));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    e->kv_tokens.push_back(prompt[n - 1]);
+    off = n;
+    st->prefill_tokens = (uint32_t)(off - reused);
+    st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    e->cached_prefill_len = n;
+    // Decode: n tokens take n-1 forwards (model.rs:1299-1337).
+    auto g0 = std::chrono::steady_clock::now();
+    hipEvent_t ea, eb;
+    HIPC(c, hipEventCreate(&ea));
+    HIPC(c, hipEventCreate(&eb));
+    HIPC(c, hipEventRecord(ea, c->stream));
+    // ids[i] is the token sampled after i forwards; forward i+1 evaluates it.
+    size_t launched = 0;
+    std::vector<uint32_t> host_ids;
+    const size_t max_gen = o->max_tokens;
+    const size_t fwd_cap = max_gen > 0 ? max_gen - 1 : 0;     // `i + 1 == max_gen` breaks first
+    const size_t ctx_cap = e->n_ctx > n ? e->n_ctx - n : 0;  // `pos >= n_ctx` stops
+    const size_t want_fwd = std::min(fwd_cap, ctx_cap);
+    size_t i = 0;
+    bool done = (max_gen == 0);
+    while (!done) {
+        // launch up to kDecodeChunk forwards ahead, then read the ids back
+        size_t target = std::min(want_fwd, launched + kDecodeChunk);
+        while (launched < target) {
+            HIPC(c, run_step(c, *e, STEP_DECODE));
+            launched++;
+        }
+        host_ids.resize(launched + 1);
+        HIPC(c, hipMemcpyAsync(host_ids.data(), e->ids, (launched + 1) * 4, hipMemcpyDeviceToHost, c->stream));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        while (!done && i <= launched) {
+            if (c->stop.load()) { snprintf(st->stop, sizeof st->stop, "user_stop"); done = true; break; }
+            const uint32_t tok = host_ids[i];
+            bool eog = false;
+            for (uint32_t x : e->eos) eog |= (x == tok);
+            if (eog) { snprintf(st->stop, sizeof st->stop, "eog"); done = true; break; }
+            gen_ids[st->gen_tokens++] = tok;
+            if (i + 1 == max_gen) { done = true; break; }
+            if (n + i >= e->n_ctx) { snprintf(st->stop, sizeof st->stop, "context_full"); done = true; break; }
+            e->kv_tokens.push_back(tok);  // forward i+1 (launched now or in the next round)
+            i++;
+        }
+    }
+    HIPC(c, hipEventRecord(eb, c->stream));
+    HIPC(c, hipEventSynchronize(eb));
+    float ms = 0.f;
+    HIPC(c, hipEventElapsedTime(&ms, ea, eb));
+    (void)hipEventDestroy(ea);
+    (void)hipEventDestroy(eb);
+    e->last_decode_us = launched ? (double)ms * 1000.0 / (double)launched : 0.0;
+    // Forwards launched past an EOS or stop only wrote KV rows beyond the
+    // recorded tokens; they are never read before being overwritten.
+    e->kv_tokens.resize(std::min(e->kv_tokens.size(), n + (size_t)st->gen_tokens));
+    if (strcmp(st->stop, "user_stop") == 0) { e->kv_tokens.clear(); e->cached_prefill_len = 0; }
+    st->gen_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - g0).count();
+    return PI_OK;
+}
+
+int pi_hip_kv_write(pi_ctx *c, uint32_t layer, uint32_t h, uint32_t pos0, uint32_t n, const float *k, const float *v) {
+    if (!c || !k || !v) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (layer >= e->n_layer || h >= e->n_kv || (uint64_t)pos0 + n > e->n_ctx) return fail(c, PI_E_INVALID, "KV range");
+    uint64_t off = (((uint64_t)layer * e->n_kv + h) * e->n_ctx + pos0) * e->dh;
+    HIPC(c, hipMemcpy(e->kc + off, k, (size_t)n * e->dh * 4, hipMemcpyHostToDevice));
+    HIPC(c, hipMemcpy(e->vc + off, v, (size_t)n * e->dh * 4, hipMemcpyHostToDevice));
+    e->kv_tokens.clear();
+    e->cached_prefill_len = 0;
+    return PI_OK;
+}
+
+int pi_hip_kv_read(pi_ctx *c, uint32_t layer, uint32_t h, uint32_t pos0, uint32_t n, float *k, float *v) {
+    if (!c || !k || !v) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (layer >= e->n_layer || h >= e->n_kv || (uint64_t)pos0 + n > e->n_ctx) return fail(c, PI_E_INVALID, "KV range");
+    uint64_t off = (((uint64_t)layer * e->n_kv + h) * e->n_ctx + pos0) * e->dh;
+    HIPC(c, hipStreamSynchronize(c->stream));
+    HIPC(c, hipMemcpy(k, e->kc + off, (size_t)n * e->dh * 4, hipMemcpyDeviceToHost));
+    HIPC(c, hipMemcpy(v, e->vc + off, (size_t)n * e->dh * 4, hipMemcpyDeviceToHost));
+    return PI_OK;
+}
+
+int pi_hip_kv_fill_normal(pi_ctx *c, uint32_t n, uint64_t seed) {
+    if (!c) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (n > e->n_ctx) return fail(c, PI_E_INVALID, "KV range");
+    HIPC(c, pi_launch_kv_fill(e->kc, e->vc, e->n_layer * e->n_kv, e->n_ctx, e->dh, n, seed, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    e->kv_tokens.clear();
+    e->cached_prefill_len = 0;
+    return PI_OK;
+}
+
+int pi_hip_kv_set_tokens(pi_ctx *c, const uint32_t *ids, uint32_t n) {
+    if (!c || (!ids && n)) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (n > e->n_ctx) return fail(c, PI_E_INVALID, "KV range");
+    e->kv_tokens.assign(ids, ids + n);
+    e->cached_prefill_len = n;
+    return PI_OK;
+}
+
+}  // extern "C"

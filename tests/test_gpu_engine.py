@@ -1,0 +1,136 @@
+"""GPU parity of the whole-forward engine against the CPU oracle.
+
+Tiny models check logits (1e-3 relative + 1e-4 absolute, the contract's
+tolerance) and greedy ids against the oracle run in the same process; the
+full-size synthetic MiniCPM-2B model checks the first 64 greedy ids against
+the committed oracle fixture tests/golden/minicpm2b_greedy.json.
+"""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).parent / "golden" / "minicpm2b_greedy.json"
+
+
+@pytest.fixture(scope="module")
+def tiny(pih):
+    return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000), seed=7)
+
+
+def _close(got, want, rtol=1e-3, atol=1e-4):
+    err = np.abs(got - want) - (atol + rtol * np.abs(want))
+    return float(err.max())
+
+
+def _bits_equal(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def test_tiny_forward_logits(pih, backend, oracle, tiny):
+    """Batch-1 forwards: logits within the contract's tolerance, and in fact
+    bit-identical since every float op keeps the reference order."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=128)
+    ref = oracle.OracleEngine(tiny, n_ctx=128, threads=4)
+    ids = [5, 17, 999, 0, 123, 456, 7, 8] + [(i * 131 + 3) % 1000 for i in range(70)]
+    for pos, tok in enumerate(ids):
+        eng.forward([tok], [pos], want_logits=True)
+        ref.forward([tok], [pos], want_logits=True)
+        got, want = eng.logits(), ref.logits()
+        assert _close(got, want) <= 0.0, f"pos {pos}: max excess {_close(got, want)}"
+        assert _bits_equal(got, want), f"pos {pos}"
+
+
+def test_tiny_batched_forward_matches_oracle(pih, backend, oracle, tiny):
+    """A batch of more than one token takes the reference's scalar order
+    (model.rs:812-822, 1028-1038); a batch of one the NEON order."""
+    for b in (10, 1):
+        eng = pih.HipEngine(backend, tiny, n_ctx=64)
+        ref = oracle.OracleEngine(tiny, n_ctx=64, threads=4)
+        ids = list(range(3, 13))
+        for off in range(0, 10, b):
+            eng.forward(ids[off:off + b], list(range(off, off + b)), want_logits=True)
+            ref.forward(ids[off:off + b], list(range(off, off + b)), want_logits=True)
+        assert _bits_equal(eng.logits(), ref.logits()), f"b={b}"
+
+
+def test_tiny_kv_rows_match_oracle(pih, backend, oracle, tiny):
+    eng = pih.HipEngine(backend, tiny, n_ctx=32)
+    ref = oracle.OracleEngine(tiny, n_ctx=32, threads=4)
+    ids = [3, 1, 4, 1, 5]
+    eng.forward(ids, list(range(5)), want_logits=False)
+    ref.forward(ids, list(range(5)), want_logits=False)
+    kr, vr = ref.kv()
+    for layer in range(tiny.spec.n_layer):
+        for h in range(tiny.spec.n_head_kv):
+            k, v = eng.kv_read(layer, h, 0, 5)
+            assert _bits_equal(k, kr[layer, h, :5]) and _bits_equal(v, vr[layer, h, :5]), (layer, h)
+
+
+@pytest.mark.parametrize("n_prompt", [45, 33, 64, 1])
+def test_tiny_generate_matches_oracle(pih, backend, oracle, tiny, n_prompt):
+    """Prefill chunks of 32 (the last one partial, or a single token), then
+    greedy decode; ids and final logits equal the oracle's generate."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=256)
+    ref = oracle.OracleEngine(tiny, n_ctx=256, threads=4)
+    prompt = [(i * 37 + 11) % 1000 for i in range(n_prompt)]
+    got, st = eng.generate(prompt, 40)
+    want, st_ref = ref.generate(prompt, 40)
+    assert got == want
+    assert st["stop"] == st_ref["stop"]
+    assert st["prefill_tokens"] == n_prompt and st["prefill_cached_tokens"] == 0
+    assert _bits_equal(eng.logits(), ref.logits())
+
+
+def test_tiny_prefix_reuse(pih, backend, oracle, tiny):
+    """tests/prefix_cache.rs:27-63 invariants on the device engine."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=256)
+    base = [(i * 13 + 5) % 997 for i in range(70)]
+    ext = base + [(i * 7 + 1) % 991 for i in range(40)]
+    eng.generate(base, 2)
+    ids, st = eng.generate(ext, 4)
+    assert st["prefill_cached_tokens"] == 64          # min(common 70, cached 70, 109) // 32 * 32
+    assert st["prefill_cached_tokens"] + st["prefill_tokens"] == len(ext)
+    fresh = pih.HipEngine(backend, tiny, n_ctx=256)
+    ids2, st2 = fresh.generate(ext, 4)
+    assert ids == ids2 and st2["prefill_cached_tokens"] == 0
+    ref_ids, _ = oracle.OracleEngine(tiny, n_ctx=256, threads=4).generate(ext, 4)
+    assert ids == ref_ids
+    # a manual forward invalidates reuse (model.rs:825-831)
+    eng.forward([ext[0]], [0], want_logits=False)
+    ids3, st3 = eng.generate(ext, 4)
+    assert st3["prefill_cached_tokens"] == 0 and ids3 == ids
+    # stop request -> user_stop, then a clean retry
+    eng.request_stop()
+    _, st4 = eng.generate(ext, 4)
+    assert st4["stop"] == "user_stop"
+    eng.clear_stop()
+    ids5, st5 = eng.generate(ext, 4)
+    assert st5["prefill_cached_tokens"] == 0 and ids5 == ids
+
+
+def test_tiny_context_full_and_eog(pih, backend, oracle, tiny):
+    eng = pih.HipEngine(backend, tiny, n_ctx=50)
+    ref = oracle.OracleEngine(tiny, n_ctx=50, threads=4)
+    prompt = list(range(40))
+    got, st = eng.generate(prompt, 30)
+    want, st_ref = ref.generate(prompt, 30)
+    assert got == want and st["stop"] == st_ref["stop"] == "context_full"
+    with pytest.raises(pih.PiError):
+        eng.forward([1], [50])
+
+
+def test_minicpm2b_first_64_greedy_ids(pih, backend):
+    """Full-size synthetic model; ids from the committed oracle fixture."""
+    g = json.loads(GOLDEN.read_text())
+    spec = pih.minicpm2b_spec()
+    model = pih.synth_model(spec, g["model_seed"])
+    import hashlib
+    for name, h in g["tensor_sha256"].items():
+        assert hashlib.sha256(model.tensors[name][3].tobytes()).hexdigest() == h, name
+    eng = pih.HipEngine(backend, model, n_ctx=len(g["prompt"]) + g["n_gen"] + 8)
+    ids, st = eng.generate(g["prompt"], g["n_gen"])
+    assert ids == g["gen_ids"], f"first mismatch at {next(i for i, (a, b) in enumerate(zip(ids, g['gen_ids'])) if a != b)}"

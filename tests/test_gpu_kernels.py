@@ -1,0 +1,151 @@
+"""GPU parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Contract: Q8 activation quants and per-block integer
+sums bit-exact; GEMV outputs within 1e-3 relative + 1e-4 absolute.  The GEMV
+kernels keep the reference's float order, so outputs are also checked bitwise.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+Q4_0, Q8_0, Q4_K, Q6_K = 2, 8, 12, 14
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def _rows(pih, t, rows, k, seed):
+    if t == Q4_K:
+        return pih.synth_q4k_random(seed, rows, k)
+    if t == Q6_K:
+        return pih.synth_q6k_random(seed, rows, k)
+    return pih.synth_tensor(seed, t, rows, k, 0.0, 0.02)
+
+
+def test_probe_name_supports_selftest(pih, backend):
+    assert pih.probe() is not None and "gfx950" in pih.probe()
+    assert "gfx950" in backend.name()
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+        assert backend.supports(t)
+    for t in (0, 1, 3, 6, 7, 10, 11, 13, 15, 30):
+        assert not backend.supports(t)
+    backend.selftest()
+
+
+@pytest.mark.parametrize("k,b", [(2304, 1), (5760, 1), (2304, 32), (256, 7), (32, 1)])
+def test_q8_quantize_bit_exact(pih, backend, oracle, k, b):
+    rng = np.random.default_rng(k * 100 + b)
+    x = rng.standard_normal(k * b).astype(np.float32)
+    x[: min(k * b, 64)] *= 1e-3            # small blocks
+    if k * b >= 256:
+        x[64:96] = 0.0                     # all-zero block -> d = 0, q = 0
+        x[96:128] = np.float32(0.5)         # halfway values
+        x[128:160] = np.linspace(-127, 127, 32, dtype=np.float32)
+    q, d, s = backend.q8_quantize(x, k, b)
+    ref = oracle.Act(x, k, b)
+    assert np.array_equal(q, ref.q)
+    assert np.array_equal(d.view(np.uint32), ref.d.view(np.uint32))
+    assert np.array_equal(s, ref.sum)
+
+
+def test_q8_quantize_halfway_vector(pih, backend, oracle):
+    """simd_q8.rs:58-80 input on the device."""
+    k = 512
+    x = ((np.arange(k) % 73).astype(np.float32) - np.float32(36.0)) * np.float32(0.0625)
+    x[0], x[1], x[2] = 127.0, 0.5, -0.5
+    q, d, s = backend.q8_quantize(x, k, 1)
+    ref = oracle.Act(x, k, 1)
+    assert q[0] == 127 and q[1] == 1 and q[2] == -1 and d[0] == 1.0
+    assert np.array_equal(q, ref.q) and np.array_equal(d.view(np.uint32), ref.d.view(np.uint32))
+    assert np.array_equal(s, ref.sum)
+
+
+CASES = [
+    (Q4_K, 5760, 2304),     # config 1 shape
+    (Q4_K, 2304, 2304),     # attn_q/k/o
+    (Q6_K, 2304, 2304),     # attn_v (Q6_K half)
+    (Q4_0, 2304, 5760),     # ffn_down (Q4_0 half)
+    (Q8_0, 2304, 5760),     # ffn_down (Q8_0 half)
+    (Q4_K, 13, 256),        # ragged tiles, one block per row
+    (Q6_K, 29, 512),
+    (Q4_0, 11, 2304),
+    (Q8_0, 5, 64),
+    (Q4_K, 1, 4096),
+]
+
+
+@pytest.mark.parametrize("t,rows,k", CASES)
+def test_block_sums_bit_exact(pih, backend, oracle, t, rows, k):
+    w = _rows(pih, t, rows, k, 100 + t)
+    x = np.random.default_rng(rows + k).standard_normal(k).astype(np.float32)
+    act = oracle.Act(x, k, 1)
+    dev = backend.upload(t, w, rows, k)
+    got = backend.block_sums(dev, act.q, act.d, act.sum)
+    rb = pih.row_bytes(t, k)
+    for r in sorted({0, rows // 2, rows - 1}):
+        want = oracle.block_sums(t, w[r * rb:(r + 1) * rb], k, act)
+        assert np.array_equal(got[r], want), f"row {r}"
+    dev.free()
+
+
+@pytest.mark.parametrize("t,rows,k", CASES)
+def test_gemv_matches_oracle(pih, backend, oracle, t, rows, k):
+    w = _rows(pih, t, rows, k, 200 + t)
+    x = np.random.default_rng(rows * 7 + k).standard_normal(k).astype(np.float32)
+    got = backend.matvec(t, w, k, x, rows)
+    act = oracle.Act(x, k, 1)
+    want = oracle.Pool(8).matmul(t, w, pih.row_bytes(t, k), k, x, 1, rows, act)
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    # same Q8 input and the reference's float order: bitwise equal
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    backend.clear_weight_cache()
+
+
+def test_gemv_config2_head(pih, backend, oracle):
+    """Q6_K output head, 122753 x 2304; x ~ N(0,1), RMS-normalised."""
+    rows, k = 122753, 2304
+    w = pih.synth_q6k_random(2, rows, k)
+    x = pih.synth_normal(22, k)
+    x = (x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5)).astype(np.float32)
+    dev = backend.upload(Q6_K, w, rows, k)
+    xd = backend.to_device(x)
+    yd = backend.alloc(rows * 4)
+    backend.gemv_dev(dev, xd.ptr, yd.ptr)
+    backend.synchronize()
+    got = yd.to_host(np.float32)
+    want = oracle.Pool(16).matmul(Q6_K, w, pih.row_bytes(Q6_K, k), k, x, 1, rows, oracle.Act(x, k, 1))
+    np.testing.assert_allclose(got, want, rtol=RTOL, atol=ATOL)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_selftest_vectors_values(pih, backend):
+    """The OpenCL self-test blocks (opencl.rs:391-430): closed forms -0.6, 5.2."""
+    x = ((np.arange(256) % 7).astype(np.float32) * np.float32(0.1) - np.float32(0.3)).astype(np.float32)
+    w4 = np.zeros(144, np.uint8)
+    w4[0:2] = (0x00, 0x3C)
+    w4[4] = 1
+    w4[16:] = 0x21
+    w6 = np.zeros(210, np.uint8)
+    w6[:128], w6[128:192], w6[192:208] = 0x95, 0x1B, 2
+    w6[208:210] = (0x00, 0x3C)
+    assert abs(backend.matvec(Q4_K, w4, 256, x, 1)[0] - (-0.6)) <= 0.6 * 0.02 + 0.01
+    assert abs(backend.matvec(Q6_K, w6, 256, x, 1)[0] - 5.2) <= 5.2 * 0.02 + 0.01
+    backend.clear_weight_cache()
+
+
+def test_fail_next_is_reported_then_clears(pih, backend):
+    w = pih.synth_q4k_random(9, 4, 256)
+    x = np.ones(256, np.float32)
+    backend.fail_next()
+    with pytest.raises(pih.PiError) as e:
+        backend.matvec(Q4_K, w, 256, x, 4)
+    assert e.value.code == -6
+    backend.matvec(Q4_K, w, 256, x, 4)
+    backend.clear_weight_cache()
+
+
+def test_matvec_rejects_bad_shapes(pih, backend):
+    w = pih.synth_q4k_random(9, 4, 256)
+    with pytest.raises(pih.PiError):
+        backend.matvec(Q4_K, w, 512, np.ones(512, np.float32), 4)
+    with pytest.raises(pih.PiError):
+        backend.matvec(0, w, 256, np.ones(256, np.float32), 4)
