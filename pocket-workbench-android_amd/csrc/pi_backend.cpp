@@ -16,6 +16,7 @@
 
 #include "pi_common.h"
 #include "pi_detmath.h"
+#include "pi_decode.h"
 #include "pi_kernels.h"
 
 struct pi_tensor {
@@ -25,7 +26,8 @@ struct pi_tensor {
 
 namespace {
 
-constexpr int kGemvMaxBlocks = 1024;   // persistent GEMV grid cap (4096 wavefronts)
+constexpr uint32_t kGemvMaxBlocks = 2048;  // persistent grid cap of the standalone GEMV (1 wave each)
+constexpr uint32_t kFusedMaxBlocks = 1024; // persistent grid cap of the fused kernels (4 waves each)
 constexpr uint32_t kMaxBatch = 64;     // model.rs:12
 constexpr uint32_t kDecodeChunk = 16;  // decode steps launched between host checks
 
@@ -38,7 +40,7 @@ struct Layer {
 struct Engine {
     uint32_t n_layer = 0, n_embd = 0, n_ff = 0, n_head = 0, n_kv = 0, dh = 0, n_rot = 0, n_vocab = 0;
     float eps = 1e-5f, theta = 10000.f;
-    uint32_t n_ctx = 0, nchunk = 0;
+    uint32_t n_ctx = 0;
     std::vector<uint32_t> eos;
     std::vector<Layer> layers;
     uint8_t *embd = nullptr;
@@ -47,10 +49,10 @@ struct Engine {
     pi_tensor *head = nullptr;
     float *out_norm = nullptr;
     float *kc = nullptr, *vc = nullptr, *cos_tab = nullptr, *sin_tab = nullptr;
-    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *attn = nullptr, *gate = nullptr,
-          *up = nullptr, *logits = nullptr, *scores = nullptr, *amax_v = nullptr;
+    float *x = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *h = nullptr, *logits = nullptr,
+          *amax_v = nullptr;
     uint32_t *amax_i = nullptr, *ids = nullptr, *prompt = nullptr;
-    int8_t *q8q = nullptr;
+    int8_t *q8q = nullptr;    // Q8 of the attention output (input of attn_o)
     float *q8d = nullptr;
     int32_t *q8s = nullptr;
     pi_state *st = nullptr;
@@ -237,10 +239,9 @@ void engine_free(Engine *e) {
     }
     free_tensor(e->head);
     for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
-                    (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->attn,
-                    (void *)e->gate, (void *)e->up, (void *)e->logits, (void *)e->scores, (void *)e->amax_v,
-                    (void *)e->amax_i, (void *)e->ids, (void *)e->prompt, (void *)e->q8q, (void *)e->q8d,
-                    (void *)e->q8s, (void *)e->st})
+                    (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->h,
+                    (void *)e->logits, (void *)e->amax_v, (void *)e->amax_i, (void *)e->ids, (void *)e->prompt,
+                    (void *)e->q8q, (void *)e->q8d, (void *)e->q8s, (void *)e->st})
         dfree(p);
     delete e;
 }
@@ -259,9 +260,9 @@ int upload_mat(pi_ctx *c, const pi_tensor_desc &t, pi_tensor **out) {
     return upload_tensor(c, t.type, t.data, (size_t)t.ne1, (size_t)t.ne0, out);
 }
 
-// A grouped GEMV launch over matrices of one type and row length.
-pi_gemv_set make_set(std::initializer_list<std::pair<const pi_tensor *, float *>> mats) {
-    pi_gemv_set S{};
+// Matrix set over tensors of one type and layout (tiles back to back).
+pi_matset make_set(std::initializer_list<std::pair<const pi_tensor *, float *>> mats) {
+    pi_matset S{};
     uint32_t t = 0, i = 0;
     for (const auto &m : mats) {
         S.w[i] = m.first->dev;
@@ -272,65 +273,94 @@ pi_gemv_set make_set(std::initializer_list<std::pair<const pi_tensor *, float *>
         i++;
     }
     S.n = i;
-    for (; i < 4; i++) S.tile0[i] = t;
+    for (uint32_t j = i; j < 4; j++) S.tile0[j] = t;
+    if (i) S.L = mats.begin()->first->L;
     return S;
 }
 
-hipError_t gemv_set(const Engine &e, std::initializer_list<std::pair<const pi_tensor *, float *>> mats, int mode,
-                    hipStream_t s) {
-    const pi_gemv_set S = make_set(mats);
-    return pi_launch_gemv_group(S, mats.begin()->first->L, e.q8q, e.q8d, e.q8s, mode, kGemvMaxBlocks, s);
+bool same_layout(const pi_tensor *a, const pi_tensor *b) {
+    return a->L.type == b->L.type && a->L.k == b->L.k && a->L.g == b->L.g;
 }
 
-// Enqueues the layers of one token: state st holds (pos, tok).
+uint32_t fused_blocks(uint32_t tiles) {
+    uint32_t b = (tiles + 3) / 4;
+    return b < 1 ? 1 : (b > kFusedMaxBlocks ? kFusedMaxBlocks : b);
+}
+
+uint32_t gemv_blocks(uint32_t tiles) { return tiles < kGemvMaxBlocks ? (tiles ? tiles : 1) : kGemvMaxBlocks; }
+
+hipError_t launch_single_gemv(const pi_tensor *w, const int8_t *q, const float *d, const int32_t *s, float *y,
+                              int32_t *sums, int mode, hipStream_t st) {
+    const pi_matset M = make_set({{w, y}});
+    return pi_launch_gemv_set(M, q, d, s, sums, mode, gemv_blocks(w->L.ntiles), st);
+}
+
+// Enqueues the layers of one token whose embedding is in x; st holds pos.
 hipError_t enqueue_layers(const Engine &e, bool neon, hipStream_t s) {
     hipError_t r;
 #define K(expr) do { if ((r = (expr)) != hipSuccess) return r; } while (0)
-    K(pi_launch_embed(e.embd, e.embd_type, e.n_embd, e.embd_row_bytes, e.st, e.x, s));
     const float scale = 1.0f / sqrtf((float)e.dh);
     for (uint32_t l = 0; l < e.n_layer; l++) {
         const Layer &L = e.layers[l];
         float *kc = e.kc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
         float *vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
-        K(pi_launch_rmsnorm_q8(e.x, L.attn_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, neon, s));
-        if (L.v->L.type == L.q->L.type && L.k->L.type == L.q->L.type) {
-            K(gemv_set(e, {{L.q, e.q}, {L.k, e.k}, {L.v, e.v}}, PI_GEMV_OUT, s));
-        } else if (L.k->L.type == L.q->L.type) {
-            K(gemv_set(e, {{L.q, e.q}, {L.k, e.k}}, PI_GEMV_OUT, s));
-            K(gemv_set(e, {{L.v, e.v}}, PI_GEMV_OUT, s));
+        // attn_norm + Q/K/V
+        pi_norm_gemv_args a{};
+        a.x = e.x; a.nw = L.attn_norm; a.ne = e.n_embd; a.eps = e.eps; a.epi = PI_EPI_OUT;
+        if (same_layout(L.q, L.k) && same_layout(L.q, L.v)) {
+            a.A = make_set({{L.q, e.q}, {L.k, e.k}, {L.v, e.v}});
+        } else if (same_layout(L.q, L.k)) {
+            a.A = make_set({{L.q, e.q}, {L.k, e.k}});
+            a.B = make_set({{L.v, e.v}});
         } else {
-            K(gemv_set(e, {{L.q, e.q}}, PI_GEMV_OUT, s));
-            K(gemv_set(e, {{L.k, e.k}}, PI_GEMV_OUT, s));
-            K(gemv_set(e, {{L.v, e.v}}, PI_GEMV_OUT, s));
+            return hipErrorInvalidValue;  // bind rejects this combination
         }
-        K(pi_launch_rope_kv(e.q, e.k, e.v, e.cos_tab, e.sin_tab, e.st, kc, vc, e.n_head, e.n_kv, e.dh, e.n_rot / 2,
-                            e.n_ctx, s));
-        K(pi_launch_attention(e.q, kc, vc, e.st, e.n_head, e.n_kv, e.dh, e.n_ctx, scale, e.scores, e.nchunk, e.attn,
-                              e.q8q, e.q8d, e.q8s, neon, s));
-        K(gemv_set(e, {{L.o, e.x}}, PI_GEMV_RESIDUAL, s));
-        K(pi_launch_rmsnorm_q8(e.x, L.ffn_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, neon, s));
-        if (L.gate->L.type == L.up->L.type) {
-            K(gemv_set(e, {{L.gate, e.gate}, {L.up, e.up}}, PI_GEMV_OUT, s));
-        } else {
-            K(gemv_set(e, {{L.gate, e.gate}}, PI_GEMV_OUT, s));
-            K(gemv_set(e, {{L.up, e.up}}, PI_GEMV_OUT, s));
-        }
-        K(pi_launch_swiglu_q8(e.gate, e.up, e.n_ff, e.q8q, e.q8d, e.q8s, s));
-        K(gemv_set(e, {{L.down, e.x}}, PI_GEMV_RESIDUAL, s));
+        a.blocks = fused_blocks(a.A.tile0[3] + a.B.tile0[3]);
+        K(pi_launch_norm_gemv(a, neon, s));
+        // RoPE + KV write + attention + Q8 of the output
+        pi_attn_args t{};
+        t.q = e.q; t.k = e.k; t.v = e.v; t.cos_tab = e.cos_tab; t.sin_tab = e.sin_tab; t.st = e.st;
+        t.kc = kc; t.vc = vc; t.n_head = e.n_head; t.n_kv = e.n_kv; t.dh = e.dh; t.n_ctx = e.n_ctx;
+        t.half = e.n_rot / 2; t.scale = scale; t.oq = e.q8q; t.od = e.q8d; t.os = e.q8s;
+        K(pi_launch_attn(t, neon, s));
+        // attn_o + residual
+        pi_gemv_res_args o{};
+        o.aq = e.q8q; o.ad = e.q8d; o.as = e.q8s; o.k = e.n_embd; o.pro = PI_PRO_GLOBAL;
+        o.M = make_set({{L.o, e.x}});
+        o.blocks = fused_blocks(o.M.tile0[3]);
+        K(pi_launch_gemv_res(o, s));
+        // ffn_norm + gate/up + SwiGLU
+        pi_norm_gemv_args f{};
+        f.x = e.x; f.nw = L.ffn_norm; f.ne = e.n_embd; f.eps = e.eps; f.epi = PI_EPI_SWIGLU; f.h = e.h;
+        f.A = make_set({{L.gate, e.h}, {L.up, e.h}});
+        f.blocks = fused_blocks(L.gate->L.ntiles);
+        K(pi_launch_norm_gemv(f, neon, s));
+        // Q8 of h + ffn_down + residual
+        pi_gemv_res_args d{};
+        d.hx = e.h; d.k = e.n_ff; d.pro = PI_PRO_Q8;
+        d.M = make_set({{L.down, e.x}});
+        d.blocks = fused_blocks(d.M.tile0[3]);
+        K(pi_launch_gemv_res(d, s));
     }
     return hipSuccess;
 }
 
+// output_norm + head GEMV (the head always normalizes one column: the batch-1
+// order, model.rs:1136-1143) with per-workgroup argmax partials.
 hipError_t enqueue_logits(const Engine &e, hipStream_t s) {
-    hipError_t r;
-    // the head always normalizes one column: the batch-1 order (model.rs:1136-1143)
-    K(pi_launch_rmsnorm_q8(e.x, e.out_norm, e.n_embd, e.eps, nullptr, e.q8q, e.q8d, e.q8s, true, s));
-    K(gemv_set(e, {{e.head, e.logits}}, PI_GEMV_OUT, s));
-    return hipSuccess;
+    pi_norm_gemv_args a{};
+    a.x = e.x; a.nw = e.out_norm; a.ne = e.n_embd; a.eps = e.eps; a.epi = PI_EPI_ARGMAX;
+    a.A = make_set({{e.head, e.logits}});
+    a.pv = e.amax_v; a.pidx = e.amax_i;
+    a.blocks = PI_HEAD_BLOCKS;
+    return pi_launch_norm_gemv(a, true, s);
 }
 
-hipError_t enqueue_argmax(const Engine &e, uint32_t *ids, hipStream_t s) {
-    return pi_launch_argmax(e.logits, e.n_vocab, e.amax_v, e.amax_i, e.st, ids, s);
+// mode: PI_STEP_ARGMAX (greedy id of the last logits), PI_STEP_PROMPT (next
+// prompt token) or PI_STEP_EMBED; then the embedding of st->tok goes to x.
+hipError_t enqueue_step(const Engine &e, int mode, uint32_t *ids, hipStream_t s) {
+    return pi_launch_step(mode, e.amax_v, e.amax_i, PI_HEAD_BLOCKS, e.st, ids, e.prompt, e.embd, e.embd_type,
+                          e.n_embd, e.embd_row_bytes, e.x, s);
 }
 #undef K
 
@@ -357,12 +387,12 @@ int build_graphs(pi_ctx *c, Engine &e) {
         HIPC(c, capture(s, neon ? &e.g_decode : &e.g_last_seq, [&] {
             hipError_t r = enqueue_layers(e, neon != 0, s);
             if (r == hipSuccess) r = enqueue_logits(e, s);
-            if (r == hipSuccess) r = enqueue_argmax(e, e.ids, s);
+            if (r == hipSuccess) r = enqueue_step(e, PI_STEP_ARGMAX, e.ids, s);
             return r;
         }));
     HIPC(c, capture(s, &e.g_prefill, [&] {
         hipError_t r = enqueue_layers(e, false, s);
-        if (r == hipSuccess) r = pi_launch_advance(e.st, e.prompt, s);
+        if (r == hipSuccess) r = enqueue_step(e, PI_STEP_PROMPT, nullptr, s);
         return r;
     }));
     return PI_OK;
@@ -386,12 +416,12 @@ hipError_t run_step(const pi_ctx *c, const Engine &e, StepKind k) {
     case STEP_LOGITS: return enqueue_logits(e, s);
     case STEP_PREFILL:
         r = enqueue_layers(e, false, s);
-        return r == hipSuccess ? pi_launch_advance(e.st, e.prompt, s) : r;
+        return r == hipSuccess ? enqueue_step(e, PI_STEP_PROMPT, nullptr, s) : r;
     case STEP_DECODE:
     case STEP_LAST_SEQ:
         r = enqueue_layers(e, k == STEP_DECODE, s);
         if (r == hipSuccess) r = enqueue_logits(e, s);
-        return r == hipSuccess ? enqueue_argmax(e, e.ids, s) : r;
+        return r == hipSuccess ? enqueue_step(e, PI_STEP_ARGMAX, e.ids, s) : r;
     }
     return hipErrorInvalidValue;
 }
@@ -513,7 +543,7 @@ size_t pi_hip_tensor_bytes(const pi_tensor *t) { return t ? (size_t)t->L.bytes :
 int pi_hip_gemv_q8_dev(pi_ctx *c, const pi_tensor *w, const int8_t *q, const float *d, const int32_t *s, float *y) {
     if (!c || !w || !q || !d || !s || !y) return PI_E_INVALID;
     if (take_injected(c)) return PI_E_INJECTED;
-    HIPC(c, pi_launch_gemv(w->dev, w->L, q, d, s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+    HIPC(c, launch_single_gemv(w, q, d, s, y, nullptr, PI_GEMV_OUT, c->stream));
     return PI_OK;
 }
 
@@ -523,7 +553,7 @@ int pi_hip_gemv_dev(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
     int r = grow_io(c, w->L.k, 1);
     if (r) return r;
     HIPC(c, pi_launch_q8(x, w->L.k, 1, c->io_q, c->io_d, c->io_s, c->stream));
-    HIPC(c, pi_launch_gemv(w->dev, w->L, c->io_q, c->io_d, c->io_s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+    HIPC(c, launch_single_gemv(w, c->io_q, c->io_d, c->io_s, y, nullptr, PI_GEMV_OUT, c->stream));
     return PI_OK;
 }
 
@@ -570,7 +600,7 @@ int pi_hip_time_gemv(pi_ctx *c, const pi_tensor *const *ws, int n_copies, const 
     HIPC(c, hipEventRecord(a, c->stream));
     for (int i = 0; i < iters; i++) {
         const pi_tensor *w = ws[i % n_copies];
-        HIPC(c, pi_launch_gemv(w->dev, w->L, q, d, s, y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks, c->stream));
+        HIPC(c, launch_single_gemv(w, q, d, s, y, nullptr, PI_GEMV_OUT, c->stream));
     }
     HIPC(c, hipEventRecord(b, c->stream));
     HIPC(c, hipEventSynchronize(b));
@@ -604,8 +634,7 @@ int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, si
     if (r) return r;
     HIPC(c, hipMemcpyAsync(c->io_x, x, k * 4, hipMemcpyHostToDevice, c->stream));
     HIPC(c, pi_launch_q8(c->io_x, (uint32_t)k, 1, c->io_q, c->io_d, c->io_s, c->stream));
-    HIPC(c, pi_launch_gemv(t->dev, t->L, c->io_q, c->io_d, c->io_s, c->io_y, nullptr, PI_GEMV_OUT, kGemvMaxBlocks,
-                           c->stream));
+    HIPC(c, launch_single_gemv(t, c->io_q, c->io_d, c->io_s, c->io_y, nullptr, PI_GEMV_OUT, c->stream));
     HIPC(c, hipMemcpyAsync(out, c->io_y, rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
     return PI_OK;
@@ -684,7 +713,7 @@ int pi_hip_block_sums(pi_ctx *c, const pi_tensor *w, const int8_t *q, const floa
     if (e == hipSuccess) e = hipMemcpyAsync(c->io_d, d, nb * 4, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(c->io_s, sum, nb * 4, hipMemcpyHostToDevice, c->stream);
     if (e == hipSuccess)
-        e = pi_launch_gemv(w->dev, w->L, c->io_q, c->io_d, c->io_s, nullptr, dsums, PI_GEMV_SUMS, kGemvMaxBlocks, c->stream);
+        e = launch_single_gemv(w, c->io_q, c->io_d, c->io_s, nullptr, dsums, PI_GEMV_SUMS, c->stream);
     if (e == hipSuccess) e = hipMemcpyAsync(sums, dsums, n * 4, hipMemcpyDeviceToHost, c->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     dfree(dsums);
@@ -726,11 +755,36 @@ int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
     }
     if (pi_type_block_elems(m->token_embd.type) == 0)
         return fail(c, PI_E_UNSUPPORTED, "token_embd type %u unsupported", m->token_embd.type);
+    // kernel coverage: Q/K (and gate/up, and the head) are super-block types
+    // with a fused norm prologue; V may differ from Q/K only between Q4_K and
+    // Q6_K; O and down take any GEMV type.
+    auto kq = [](uint32_t t) { return t == PI_TYPE_Q4_K || t == PI_TYPE_Q6_K; };
+    if (!kq(m->output.type)) return fail(c, PI_E_UNSUPPORTED, "output type %u: the head GEMV needs Q4_K or Q6_K", m->output.type);
+    for (uint32_t l = 0; l < m->n_layer; l++) {
+        const pi_layer_desc &L = m->layers[l];
+        if (!kq(L.attn_q.type) || L.attn_k.type != L.attn_q.type || !kq(L.attn_v.type))
+            return fail(c, PI_E_UNSUPPORTED, "layer %u: attn_q/attn_k/attn_v types %u/%u/%u not supported", l,
+                        L.attn_q.type, L.attn_k.type, L.attn_v.type);
+        if (!kq(L.ffn_gate.type) || L.ffn_up.type != L.ffn_gate.type)
+            return fail(c, PI_E_UNSUPPORTED, "layer %u: ffn_gate/ffn_up types %u/%u not supported", l, L.ffn_gate.type,
+                        L.ffn_up.type);
+        if (!pi_gemv_type(L.attn_o.type) || !pi_gemv_type(L.ffn_down.type))
+            return fail(c, PI_E_UNSUPPORTED, "layer %u: attn_o/ffn_down types %u/%u not supported", l, L.attn_o.type,
+                        L.ffn_down.type);
+    }
+    {
+        int dev = 0, maxlds = 0;
+        (void)hipGetDevice(&dev);
+        if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, dev) != hipSuccess || maxlds <= 0)
+            maxlds = 65536;
+        if (pi_attn_lds_bytes(n_ctx) > (size_t)maxlds)
+            return fail(c, PI_E_UNSUPPORTED, "n_ctx %u needs %zu bytes of LDS for attention (device has %d)", n_ctx,
+                        pi_attn_lds_bytes(n_ctx), maxlds);
+    }
     Engine *e = new Engine();
     e->n_layer = m->n_layer; e->n_embd = m->n_embd; e->n_ff = m->n_ff; e->n_head = m->n_head;
     e->n_kv = m->n_head_kv; e->dh = m->head_dim; e->n_rot = m->n_rot; e->n_vocab = (uint32_t)vocab;
     e->eps = m->rms_eps; e->theta = m->rope_theta; e->n_ctx = n_ctx;
-    e->nchunk = (n_ctx + 63) / 64;
     e->eos.assign(m->eos_ids, m->eos_ids + m->n_eos);
     e->layers.resize(m->n_layer);
     int r = PI_OK;
@@ -785,10 +839,9 @@ int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
     }
     const uint32_t big = e->n_embd > e->n_ff ? e->n_embd : e->n_ff;
     TRY(dalloc(c, &e->x, ne)); TRY(dalloc(c, &e->q, qdim)); TRY(dalloc(c, &e->k, kdim)); TRY(dalloc(c, &e->v, kdim));
-    TRY(dalloc(c, &e->attn, qdim)); TRY(dalloc(c, &e->gate, e->n_ff)); TRY(dalloc(c, &e->up, e->n_ff));
+    TRY(dalloc(c, &e->h, e->n_ff));
     TRY(dalloc(c, &e->logits, vocab));
-    TRY(dalloc(c, &e->scores, (size_t)e->n_head * n_ctx));
-    TRY(dalloc(c, &e->amax_v, PI_ARGMAX_BLOCKS)); TRY(dalloc(c, &e->amax_i, PI_ARGMAX_BLOCKS));
+    TRY(dalloc(c, &e->amax_v, PI_HEAD_BLOCKS)); TRY(dalloc(c, &e->amax_i, PI_HEAD_BLOCKS));
     TRY(dalloc(c, &e->ids, (size_t)n_ctx + kDecodeChunk + 2)); TRY(dalloc(c, &e->prompt, (size_t)n_ctx + 1));
     TRY(dalloc(c, &e->q8q, big)); TRY(dalloc(c, &e->q8d, big / 32)); TRY(dalloc(c, &e->q8s, big / 32));
     TRY(dalloc(c, &e->st, 1));
@@ -811,6 +864,7 @@ static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int 
         if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
         int r = set_state(c, *e, pos[i], ids[i], 0, 0);
         if (r) return r;
+        HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
         // a batch of more than one token evaluates in the scalar order (model.rs:812-822, 1028-1038)
         HIPC(c, run_step(c, *e, b > 1 ? STEP_LAYERS_SEQ : STEP_LAYERS_NEON));
     }
@@ -843,7 +897,7 @@ int pi_hip_argmax(pi_ctx *c, uint32_t *id) {
     if (!c || !id) return PI_E_INVALID;
     Engine *e = c->eng;
     if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
-    HIPC(c, enqueue_argmax(*e, nullptr, c->stream));
+    HIPC(c, enqueue_step(*e, PI_STEP_ARGMAX, nullptr, c->stream));
     pi_state h;
     HIPC(c, hipMemcpyAsync(&h, e->st, sizeof h, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
@@ -888,6 +942,7 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     HIPC(c, hipMemcpyAsync(e->prompt, prompt, n * 4, hipMemcpyHostToDevice, c->stream));
     int r = set_state(c, *e, (int32_t)reused, prompt[reused], 0, (uint32_t)reused);
     if (r) return r;
+    HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
     size_t off = reused;
     bool stopped = false;
     // Prefill in 32-token chunks from `reused` (model.rs:1269-1288).  Tokens of
