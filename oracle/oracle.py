@@ -248,6 +248,10 @@ class OracleEngine:
         if rc:
             raise RuntimeError(lib().po_last_error(self.h).decode())
 
+    def set_int8(self, enabled: bool) -> None:
+        """Engine int8 toggle (model.rs:689-694): False selects the f32 path."""
+        lib().po_engine_set_int8(self.h, int(enabled))
+
     def logits(self) -> np.ndarray:
         n = self.model.spec.n_vocab
         return np.ctypeslib.as_array(lib().po_logits(self.h), (n,)).copy()
