@@ -209,6 +209,21 @@ void pi_hip_clear_stop(pi_ctx *ctx);
 /* Engine steps replay captured HIP graphs by default; enable = 0 launches the
  * same kernels one by one (for profilers that cannot follow graph launches). */
 int  pi_hip_use_graphs(pi_ctx *ctx, int enable);
+/* Engine tokens run as one persistent cooperative kernel per token by default
+ * (stages hand data to each other through flag-tagged words in HBM); enable
+ * = 0 selects the per-stage kernels instead.  No counterpart in the
+ * reference: the reference evaluates a token as a sequence of CPU loops. */
+int  pi_hip_use_persistent(pi_ctx *ctx, int enable);
+/* 1 when the bound model runs on the persistent kernel, 0 otherwise. */
+int  pi_hip_persistent_active(const pi_ctx *ctx);
+/* Stage tracing of the persistent kernel (the reference's GenStats wall
+ * times, model.rs:666-676, at stage granularity): when enabled, every
+ * workgroup records the 100 MHz device clock at the end of each stage of the
+ * last launch.  pi_hip_stage_trace_read copies blocks*slots entries
+ * (workgroup-major: start, embedding, 5 per layer, head); out = NULL only
+ * reports blocks and slots. */
+int  pi_hip_stage_trace(pi_ctx *ctx, int enable);
+int  pi_hip_stage_trace_read(pi_ctx *ctx, uint64_t *out, size_t n, uint32_t *blocks, uint32_t *slots);
 /* Per-forward timing of the last generate call, microseconds (device events). */
 int  pi_hip_last_decode_us(pi_ctx *ctx, double *per_token_us);
 

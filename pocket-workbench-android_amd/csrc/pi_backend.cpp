@@ -18,6 +18,7 @@
 #include "pi_detmath.h"
 #include "pi_decode.h"
 #include "pi_kernels.h"
+#include "pi_mega.h"
 
 struct pi_tensor {
     pi_layout L;
@@ -63,6 +64,17 @@ struct Engine {
     std::vector<uint32_t> kv_tokens;
     size_t cached_prefill_len = 0;
     double last_decode_us = 0.0;
+    // persistent decode kernel (pi_mega.hip)
+    bool mega_ok = false;           // the model fits the kernel
+    pi_mega_args mega{};            // host copy of the device-resident arguments
+    pi_mega_args *mega_dev = nullptr;
+    pi_mega_layer *mega_layers = nullptr;
+    uint64_t *mega_words = nullptr; // flag-tagged hand-off words of every layer
+    uint64_t *mega_part = nullptr;
+    int32_t *mega_abort = nullptr;
+    uint64_t *mega_trace = nullptr;  // per-workgroup stage timestamps when tracing
+    uint32_t mega_blocks = 0, epoch = 0;
+    size_t mega_lds = 0;
 };
 
 }  // namespace
@@ -73,6 +85,7 @@ struct pi_ctx {
     std::string name, err;
     bool fail_next = false;
     bool use_graphs = true;   // replay captured graphs (else launch each kernel)
+    bool use_persistent = true;  // one persistent kernel per token when the model fits
     std::atomic<int> stop{0};
     std::map<std::pair<uintptr_t, size_t>, pi_tensor *> wcache;
     // grow-only IO buffers of matvec / test hooks (opencl.rs:461-482)
@@ -238,6 +251,9 @@ void engine_free(Engine *e) {
         dfree(l.ffn_norm);
     }
     free_tensor(e->head);
+    for (void *p : {(void *)e->mega_dev, (void *)e->mega_layers, (void *)e->mega_words, (void *)e->mega_part,
+                    (void *)e->mega_abort, (void *)e->mega_trace})
+        dfree(p);
     for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
                     (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->h,
                     (void *)e->logits, (void *)e->amax_v, (void *)e->amax_i, (void *)e->ids, (void *)e->prompt,
@@ -398,6 +414,128 @@ int build_graphs(pi_ctx *c, Engine &e) {
     return PI_OK;
 }
 
+// Kernel-side view of tensors of one layout, tiles numbered back to back.
+pig::MatSet mset(std::initializer_list<const pi_tensor *> ts) {
+    pig::MatSet S{};
+    uint32_t t = 0, i = 0;
+    for (const pi_tensor *x : ts) {
+        S.w[i] = x->dev;
+        S.y[i] = nullptr;
+        S.rows[i] = x->L.rows;
+        S.tile0[i] = t;
+        t += x->L.ntiles;
+        i++;
+    }
+    S.n = i;
+    for (uint32_t j = i; j < 4; j++) S.tile0[j] = t;
+    if (i) {
+        const pi_layout &L = (*ts.begin())->L;
+        S.upr = L.upr;
+        S.rpw = L.rpw;
+        S.lpt = L.lpt;
+        S.tile_bytes = L.tile_bytes;
+    }
+    return S;
+}
+
+// Sets up the persistent decode kernel for a bound model; leaves mega_ok
+// false (per-stage kernels are used) when the model is outside its limits.
+int build_mega(pi_ctx *c, Engine &e) {
+    e.mega_ok = false;
+    const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
+    if (e.n_embd % 128 || e.n_embd / 32 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64) return PI_OK;
+    int maxlds = 0;
+    if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;
+    e.mega_lds = pi_mega_lds_bytes(e.n_embd, e.n_ff, e.n_ctx);
+    if (e.mega_lds > (size_t)maxlds) return PI_OK;
+    e.mega_blocks = pi_mega_blocks(c->device, e.n_embd, e.n_ff, e.n_ctx);
+    if (e.mega_blocks == 0) return PI_OK;
+    const uint64_t per = pi_mega_layer_words(e.n_embd, e.n_ff, qdim, kdim);
+    int r;
+    if ((r = dalloc(c, &e.mega_words, per * e.n_layer)) || (r = dalloc(c, &e.mega_part, 2ull * e.mega_blocks)) ||
+        (r = dalloc(c, &e.mega_abort, 1)) || (r = dalloc(c, &e.mega_layers, e.n_layer)) || (r = dalloc(c, &e.mega_dev, 1)))
+        return r;
+    HIPC(c, hipMemset(e.mega_words, 0, per * e.n_layer * 8));
+    HIPC(c, hipMemset(e.mega_part, 0, 2ull * e.mega_blocks * 8));
+    HIPC(c, hipMemset(e.mega_abort, 0, 4));
+    std::vector<pi_mega_layer> ly(e.n_layer);
+    for (uint32_t l = 0; l < e.n_layer; l++) {
+        const Layer &L = e.layers[l];
+        pi_mega_layer &Y = ly[l];
+        memset(&Y, 0, sizeof Y);
+        if (same_layout(L.q, L.k) && same_layout(L.q, L.v)) {
+            Y.qkv = mset({L.q, L.k, L.v});
+        } else {
+            Y.qkv = mset({L.q, L.k});
+            Y.vb = mset({L.v});
+        }
+        Y.t_qkv = L.q->L.type;
+        Y.t_vb = L.v->L.type;
+        Y.o = mset({L.o});
+        Y.t_o = L.o->L.type;
+        Y.g_o = L.o->L.g;
+        Y.gu = mset({L.gate, L.up});
+        Y.t_gu = L.gate->L.type;
+        Y.down = mset({L.down});
+        Y.t_down = L.down->L.type;
+        Y.g_down = L.down->L.g;
+        Y.attn_norm = L.attn_norm;
+        Y.ffn_norm = L.ffn_norm;
+        Y.kc = e.kc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        Y.vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        uint64_t *w = e.mega_words + per * l;
+        Y.q = w; w += qdim;
+        Y.k = w; w += kdim;
+        Y.v = w; w += kdim;
+        Y.att = w; w += qdim / 4 + qdim / 16;
+        Y.xb = w; w += e.n_embd;
+        Y.h = w; w += e.n_ff;
+        Y.xo = w;
+    }
+    HIPC(c, hipMemcpy(e.mega_layers, ly.data(), ly.size() * sizeof(pi_mega_layer), hipMemcpyHostToDevice));
+    pi_mega_args &a = e.mega;
+    memset(&a, 0, sizeof a);
+    a.layers = e.mega_layers;
+    a.n_layer = e.n_layer; a.ne = e.n_embd; a.n_ff = e.n_ff; a.n_head = e.n_head; a.n_kv = e.n_kv;
+    a.half = e.n_rot / 2; a.n_ctx = e.n_ctx;
+    a.eps = e.eps; a.scale = 1.0f / sqrtf((float)e.dh);
+    a.cos_tab = e.cos_tab; a.sin_tab = e.sin_tab;
+    a.embd = e.embd; a.erow_bytes = e.embd_row_bytes; a.etype = e.embd_type;
+    a.head = mset({e.head});
+    a.t_head = e.head->L.type;
+    a.out_norm = e.out_norm;
+    a.logits = e.logits;
+    a.part = e.mega_part;
+    a.tok_state = &e.st->tok;
+    a.abort_flag = e.mega_abort;
+    a.trace = nullptr;
+    HIPC(c, hipMemcpy(e.mega_dev, &a, sizeof a, hipMemcpyHostToDevice));
+    e.mega_ok = true;
+    return PI_OK;
+}
+
+bool use_mega(const pi_ctx *c, const Engine &e) { return c->use_persistent && e.mega_ok; }
+
+// One token through the persistent kernel (layers, and the head when `head`).
+hipError_t mega_token(const pi_ctx *c, Engine &e, int32_t pos, uint32_t tok_imm, const uint32_t *tok_src,
+                      uint32_t *id_out, bool neon, bool head) {
+    if (++e.epoch == 0) e.epoch = 1;
+    pi_mega_launch l{tok_src, id_out, tok_imm, pos, e.epoch};
+    return pi_launch_mega(e.mega, e.mega_dev, l, neon, head, e.mega_blocks, e.mega_lds, c->stream);
+}
+
+// Reads and clears the abort flag after the stream has drained.
+int mega_check(pi_ctx *c, Engine &e) {
+    if (!use_mega(c, e)) return PI_OK;
+    int32_t f = 0;
+    HIPC(c, hipMemcpy(&f, e.mega_abort, 4, hipMemcpyDeviceToHost));
+    if (f) {
+        HIPC(c, hipMemset(e.mega_abort, 0, 4));
+        return fail(c, PI_E_HIP, "persistent decode kernel: a hand-off wait exceeded its bound");
+    }
+    return PI_OK;
+}
+
 enum StepKind { STEP_LAYERS_NEON, STEP_LAYERS_SEQ, STEP_LOGITS, STEP_DECODE, STEP_PREFILL, STEP_LAST_SEQ };
 
 // One engine step on the context stream: a graph replay, or the same kernels
@@ -519,6 +657,45 @@ int pi_hip_synchronize(pi_ctx *c) {
 int pi_hip_use_graphs(pi_ctx *c, int enable) {
     if (!c) return PI_E_INVALID;
     c->use_graphs = enable != 0;
+    return PI_OK;
+}
+
+int pi_hip_use_persistent(pi_ctx *c, int enable) {
+    if (!c) return PI_E_INVALID;
+    c->use_persistent = enable != 0;
+    return PI_OK;
+}
+
+int pi_hip_persistent_active(const pi_ctx *c) { return c && c->eng && use_mega(c, *c->eng) ? 1 : 0; }
+
+int pi_hip_stage_trace(pi_ctx *c, int enable) {
+    if (!c) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
+    if (!e->mega_ok) return fail(c, PI_E_UNSUPPORTED, "the bound model does not run on the persistent kernel");
+    HIPC(c, hipStreamSynchronize(c->stream));
+    if (enable && !e->mega_trace) {
+        const size_t n = (size_t)e->mega_blocks * pi_mega_trace_slots(e->n_layer);
+        int r = dalloc(c, &e->mega_trace, n);
+        if (r) return r;
+        HIPC(c, hipMemset(e->mega_trace, 0, n * 8));
+    }
+    e->mega.trace = enable ? e->mega_trace : nullptr;
+    HIPC(c, hipMemcpy(e->mega_dev, &e->mega, sizeof e->mega, hipMemcpyHostToDevice));
+    return PI_OK;
+}
+
+int pi_hip_stage_trace_read(pi_ctx *c, uint64_t *out, size_t n, uint32_t *blocks, uint32_t *slots) {
+    if (!c || !blocks || !slots) return PI_E_INVALID;
+    Engine *e = c->eng;
+    if (!e || !e->mega_trace) return fail(c, PI_E_INVALID, "stage tracing is off");
+    *blocks = e->mega_blocks;
+    *slots = pi_mega_trace_slots(e->n_layer);
+    const size_t need = (size_t)*blocks * *slots;
+    if (!out) return PI_OK;
+    if (n < need) return fail(c, PI_E_INVALID, "trace needs %zu entries", need);
+    HIPC(c, hipStreamSynchronize(c->stream));
+    HIPC(c, hipMemcpy(out, e->mega_trace, need * 8, hipMemcpyDeviceToHost));
     return PI_OK;
 }
 
@@ -847,6 +1024,7 @@ int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
     TRY(dalloc(c, &e->st, 1));
     if (hipMemset(e->logits, 0, vocab * 4) != hipSuccess) { engine_free(e); return fail(c, PI_E_HIP, "memset"); }
     TRY(build_graphs(c, *e));
+    TRY(build_mega(c, *e));
 #undef TRY
     c->eng = e;
     return PI_OK;
@@ -859,6 +1037,14 @@ static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int 
         if (pos[i] < 0 || (uint32_t)pos[i] >= e->n_ctx) return fail(c, PI_E_CONTEXT_FULL, "context full");
         if (ids[i] >= e->n_vocab) return fail(c, PI_E_INVALID, "token %u out of vocab", ids[i]);
         if (i > 0 && pos[i] <= pos[i - 1]) return fail(c, PI_E_INVALID, "batch positions must increase");
+    }
+    if (use_mega(c, *e)) {
+        for (int i = 0; i < b; i++) {
+            if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
+            HIPC(c, mega_token(c, *e, pos[i], ids[i], nullptr, nullptr, b == 1, want_logits && i == b - 1));
+        }
+        HIPC(c, hipStreamSynchronize(c->stream));
+        return mega_check(c, *e);
     }
     for (int i = 0; i < b; i++) {
         if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
@@ -897,7 +1083,8 @@ int pi_hip_argmax(pi_ctx *c, uint32_t *id) {
     if (!c || !id) return PI_E_INVALID;
     Engine *e = c->eng;
     if (!e) return fail(c, PI_E_NOMODEL, "no model bound");
-    HIPC(c, enqueue_step(*e, PI_STEP_ARGMAX, nullptr, c->stream));
+    // the persistent kernel leaves the greedy id of its last head in the state
+    if (!use_mega(c, *e)) HIPC(c, enqueue_step(*e, PI_STEP_ARGMAX, nullptr, c->stream));
     pi_state h;
     HIPC(c, hipMemcpyAsync(&h, e->st, sizeof h, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
@@ -939,10 +1126,11 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     e->kv_tokens.resize(reused);
     e->cached_prefill_len = 0;
     st->prefill_cached_tokens = (uint32_t)reused;
+    const bool mega = use_mega(c, *e);
     HIPC(c, hipMemcpyAsync(e->prompt, prompt, n * 4, hipMemcpyHostToDevice, c->stream));
     int r = set_state(c, *e, (int32_t)reused, prompt[reused], 0, (uint32_t)reused);
     if (r) return r;
-    HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
+    if (!mega) HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
     size_t off = reused;
     bool stopped = false;
     // Prefill in 32-token chunks from `reused` (model.rs:1269-1288).  Tokens of
@@ -952,8 +1140,12 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     while (off + 1 < n) {
         if (c->stop.load()) { stopped = true; break; }
         size_t end = std::min(n - 1, off + chunk);
-        for (size_t t = off; t < end; t++) HIPC(c, run_step(c, *e, STEP_PREFILL));
+        for (size_t t = off; t < end; t++) {
+            if (mega) HIPC(c, mega_token(c, *e, (int32_t)t, prompt[t], nullptr, nullptr, false, false));
+            else HIPC(c, run_step(c, *e, STEP_PREFILL));
+        }
         HIPC(c, hipStreamSynchronize(c->stream));
+        if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); return r; }
         e->kv_tokens.insert(e->kv_tokens.end(), prompt + off, prompt + end);
         off = end;
     }
@@ -965,8 +1157,10 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
         st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
         return PI_OK;
     }
-    HIPC(c, run_step(c, *e, last_chunk > 1 ? STEP_LAST_SEQ : STEP_DECODE));
+    if (mega) HIPC(c, mega_token(c, *e, (int32_t)(n - 1), prompt[n - 1], nullptr, e->ids, last_chunk == 1, true));
+    else HIPC(c, run_step(c, *e, last_chunk > 1 ? STEP_LAST_SEQ : STEP_DECODE));
     HIPC(c, hipStreamSynchronize(c->stream));
+    if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); return r; }
     e->kv_tokens.push_back(prompt[n - 1]);
     off = n;
     st->prefill_tokens = (uint32_t)(off - reused);
@@ -991,12 +1185,15 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
         // launch up to kDecodeChunk forwards ahead, then read the ids back
         size_t target = std::min(want_fwd, launched + kDecodeChunk);
         while (launched < target) {
-            HIPC(c, run_step(c, *e, STEP_DECODE));
+            if (mega)
+                HIPC(c, mega_token(c, *e, (int32_t)(n + launched), 0, &e->st->tok, e->ids + launched + 1, true, true));
+            else HIPC(c, run_step(c, *e, STEP_DECODE));
             launched++;
         }
         host_ids.resize(launched + 1);
         HIPC(c, hipMemcpyAsync(host_ids.data(), e->ids, (launched + 1) * 4, hipMemcpyDeviceToHost, c->stream));
         HIPC(c, hipStreamSynchronize(c->stream));
+        if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); e->cached_prefill_len = 0; return r; }
         while (!done && i <= launched) {
             if (c->stop.load()) { snprintf(st->stop, sizeof st->stop, "user_stop"); done = true; break; }
             const uint32_t tok = host_ids[i];

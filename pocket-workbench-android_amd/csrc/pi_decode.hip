@@ -155,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void k_norm_gemv(const float *__restrict_
     ActLds A = carve_act(reinterpret_cast<unsigned char *>(xs + xs_floats(ne)), ne);
 
     const uint32_t gw = blockIdx.x * (kThreads / 64) + wave, nw_all = gridDim.x * (kThreads / 64);
-    const uint32_t ntA = SA.tile0[SA.n];
+    const uint32_t ntA = SA.tile0[3];
     float best_v = -INFINITY;
     uint32_t best_i = 0xFFFFFFFFu;
 
@@ -269,7 +269,7 @@ __global__ __launch_bounds__(kThreads) void k_gemv_res(const int8_t *__restrict_
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     float *strip = reinterpret_cast<float *>(smem) + wave * 64 * TPU;
     const uint32_t gw = blockIdx.x * (kThreads / 64) + wave, nw_all = gridDim.x * (kThreads / 64);
-    const uint32_t nt = S.tile0[S.n];
+    const uint32_t nt = S.tile0[3];
     const TileRef R0 = tile_ref(S, gw < nt ? gw : nt - 1);
     Unit<T, G> U0;
     U0.load(R0.base, R0.lanes, min(lane, R0.lanes - 1));
@@ -459,48 +459,6 @@ __global__ __launch_bounds__(kThreads) void k_attn(const float *__restrict__ qv,
 // token.  MODE_EMBED: keep the state.  Then embed st->tok into x
 // (dequant_row of token_embd, model.rs:857-869).
 // ---------------------------------------------------------------------------
-__device__ float embed_elem(const uint8_t *row, uint32_t type, uint32_t e) {
-    float v = 0.0f;
-    if (type == PI_TYPE_F32) {
-        memcpy(&v, row + 4 * (uint64_t)e, 4);
-    } else if (type == PI_TYPE_Q4_K) {
-        const uint8_t *b = row + (uint64_t)(e / 256) * 144;
-        const uint32_t j = e % 256, g = j / 64, hi = (j % 64) >= 32, l = j % 32, is = 2 * g + hi;
-        const float dd = h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8)), dm = h2f((uint32_t)b[2] | ((uint32_t)b[3] << 8));
-        const uint8_t *sc = b + 4;
-        uint32_t s, m;
-        if (is < 4) {
-            s = sc[is] & 63u;
-            m = sc[is + 4] & 63u;
-        } else {
-            s = (sc[is + 4] & 0xFu) | ((sc[is - 4] >> 6) << 4);
-            m = (sc[is + 4] >> 4) | ((sc[is] >> 6) << 4);
-        }
-        const uint32_t qv = hi ? (b[16 + g * 32 + l] >> 4) : (b[16 + g * 32 + l] & 0xFu);
-        const float d1 = dd * (float)s, m1 = dm * (float)m;
-        v = d1 * (float)qv - m1;
-    } else if (type == PI_TYPE_Q6_K) {
-        const uint8_t *b = row + (uint64_t)(e / 256) * 210;
-        const uint32_t j = e % 256, hf = j / 128, r = j % 128, s4 = r / 32, l = r % 32;
-        uint32_t qlv = b[hf * 64 + l + (s4 & 1u) * 32];
-        qlv = (s4 >= 2) ? (qlv >> 4) : (qlv & 0xFu);
-        const uint32_t qhv = (b[128 + hf * 32 + l] >> (2 * s4)) & 3u;
-        const int qq = (int)(qlv | (qhv << 4)) - 32;
-        const float dd = h2f((uint32_t)b[208] | ((uint32_t)b[209] << 8));
-        const float scv = (float)(int8_t)b[192 + hf * 8 + l / 16 + 2 * s4];
-        v = dd * scv * (float)qq;
-    } else if (type == PI_TYPE_Q4_0) {
-        const uint8_t *b = row + (uint64_t)(e / 32) * 18;
-        const uint32_t j = e % 32;
-        const uint32_t qv = j < 16 ? (b[2 + j] & 0xFu) : (b[2 + j - 16] >> 4);
-        v = ((float)qv - 8.0f) * h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
-    } else if (type == PI_TYPE_Q8_0) {
-        const uint8_t *b = row + (uint64_t)(e / 32) * 34;
-        v = (float)(int8_t)b[2 + e % 32] * h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
-    }
-    return v;
-}
-
 template <int MODE>
 __global__ __launch_bounds__(kThreads) void k_step(const float *__restrict__ pv, const uint32_t *__restrict__ pidx,
                                                    uint32_t np, pi_state *__restrict__ st, uint32_t *__restrict__ ids,

@@ -22,6 +22,29 @@
 
 namespace pig {
 
+// Global-memory views of generic pointers.  Pointers read from memory (rather
+// than passed as kernel arguments) are generic to the compiler, which then
+// emits flat loads; a flat load counts on both the vector-memory and the LDS
+// wait counters, so any later LDS access waits for every outstanding weight
+// load.  Casting to the global address space gives global loads.
+// (The host pass of a HIP compile also parses device functions; it never runs
+// them and has no address spaces, so the qualifier is applied only when
+// compiling for the device.)
+#if defined(__HIP_DEVICE_COMPILE__)
+#define PI_GLOBAL __attribute__((address_space(1)))
+#define PI_CONSTANT __attribute__((address_space(4)))
+#else
+#define PI_GLOBAL
+#define PI_CONSTANT
+#endif
+template <typename T> __device__ __forceinline__ const PI_GLOBAL T *gld(const T *p) { return (const PI_GLOBAL T *)p; }
+template <typename T> __device__ __forceinline__ PI_GLOBAL T *gst(T *p) { return (PI_GLOBAL T *)p; }
+// Copy of a descriptor that no thread writes during the kernel, read through
+// the constant address space so the fields come in with scalar loads.
+template <typename T> __device__ __forceinline__ T cload(const T *p) {
+    return *(const PI_CONSTANT T *)p;
+}
+
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 __device__ __forceinline__ float h2f(uint32_t bits) { return pi_f16_to_f32((uint16_t)(bits & 0xFFFFu)); }
 __device__ __forceinline__ int comp(const int4 &v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
@@ -147,9 +170,9 @@ template <uint32_t T, int G> struct Unit {
     __device__ __forceinline__ void load(const uint8_t *tb, uint32_t lanes, uint32_t l) {
 #pragma unroll
         for (int j = 0; j < QC; j++)
-            c[j] = *reinterpret_cast<const int4 *>(tb + ((uint64_t)j * lanes + l) * 16u);
+            c[j] = *gld(reinterpret_cast<const int4 *>(tb + ((uint64_t)j * lanes + l) * 16u));
         if constexpr (QT<T>::DF) {
-            const uint16_t *dp = reinterpret_cast<const uint16_t *>(tb + (uint64_t)lanes * QC * 16u);
+            const PI_GLOBAL uint16_t *dp = gld(reinterpret_cast<const uint16_t *>(tb + (uint64_t)lanes * QC * 16u));
 #pragma unroll
             for (int b = 0; b < G; b++) db[b] = dp[(uint64_t)b * lanes + l];
         }
@@ -278,7 +301,8 @@ __device__ __forceinline__ void unit_terms(const Unit<T, G> &U, const Slice<T, G
 
 // ---------------------------------------------------------------------------
 // Matrices of one type and layout that share an activation, tiles numbered
-// back to back (tile0[m] = first tile of matrix m, tile0[n] = total).
+// back to back (tile0[m] = first tile of matrix m; tile0[j] = total for
+// every j >= n, so tile0[3] is always the total).
 // ---------------------------------------------------------------------------
 struct MatSet {
     const uint8_t *w[3];
@@ -295,6 +319,34 @@ struct TileRef {
     uint32_t m, tile, lanes, row0, nrows;
 };
 
+// A MatSet is read either from a value (kernel argument) or, through SetRef,
+// from device memory with scalar loads at each use, so that persistent
+// kernels keep no descriptor fields live in registers.
+struct SetRef {
+    const MatSet *p;
+};
+__device__ __forceinline__ uint32_t ms_n(const MatSet &S) { return S.n; }
+__device__ __forceinline__ uint32_t ms_t0(const MatSet &S, int i) { return S.tile0[i]; }
+__device__ __forceinline__ uint32_t ms_rows(const MatSet &S, int i) { return S.rows[i]; }
+__device__ __forceinline__ const uint8_t *ms_w(const MatSet &S, int i) { return S.w[i]; }
+__device__ __forceinline__ uint32_t ms_upr(const MatSet &S) { return S.upr; }
+__device__ __forceinline__ uint32_t ms_rpw(const MatSet &S) { return S.rpw; }
+__device__ __forceinline__ uint32_t ms_lpt(const MatSet &S) { return S.lpt; }
+__device__ __forceinline__ uint64_t ms_tb(const MatSet &S) { return S.tile_bytes; }
+__device__ __forceinline__ uint32_t ms_n(const SetRef &S) { return cload(&S.p->n); }
+__device__ __forceinline__ uint32_t ms_t0(const SetRef &S, int i) { return cload(&S.p->tile0[i]); }
+__device__ __forceinline__ uint32_t ms_rows(const SetRef &S, int i) { return cload(&S.p->rows[i]); }
+__device__ __forceinline__ const uint8_t *ms_w(const SetRef &S, int i) { return cload(&S.p->w[i]); }
+__device__ __forceinline__ uint32_t ms_upr(const SetRef &S) { return cload(&S.p->upr); }
+__device__ __forceinline__ uint32_t ms_rpw(const SetRef &S) { return cload(&S.p->rpw); }
+__device__ __forceinline__ uint32_t ms_lpt(const SetRef &S) { return cload(&S.p->lpt); }
+__device__ __forceinline__ uint64_t ms_tb(const SetRef &S) { return cload(&S.p->tile_bytes); }
+// total tiles (tile0[j] = total for every j >= n)
+template <typename SS> __device__ __forceinline__ uint32_t ms_total(const SS &S) { return ms_t0(S, 3); }
+
+// Tile reference of global tile gt.  A MatSet value (a kernel argument, in
+// constant memory) is indexed with the matrix number; through a SetRef the
+// fields are read with scalar loads and chosen with selects.
 __device__ __forceinline__ TileRef tile_ref(const MatSet &S, uint32_t gt) {
     TileRef r;
     uint32_t m = 0;
@@ -310,18 +362,67 @@ __device__ __forceinline__ TileRef tile_ref(const MatSet &S, uint32_t gt) {
     return r;
 }
 
+__device__ __forceinline__ TileRef tile_ref(const SetRef &S, uint32_t gt) {
+    TileRef r;
+    const uint32_t n = ms_n(S), t1_ = ms_t0(S, 1), t2_ = ms_t0(S, 2);
+    const uint32_t m = (n > 2 && gt >= t2_) ? 2u : ((n > 1 && gt >= t1_) ? 1u : 0u);
+    const uint32_t t0 = m == 0 ? ms_t0(S, 0) : (m == 1 ? t1_ : t2_);
+    const uint32_t t1 = m == 0 ? t1_ : (m == 1 ? t2_ : ms_t0(S, 3));
+    const uint32_t rows = m == 0 ? ms_rows(S, 0) : (m == 1 ? ms_rows(S, 1) : ms_rows(S, 2));
+    const uint8_t *w = m == 0 ? ms_w(S, 0) : (m == 1 ? ms_w(S, 1) : ms_w(S, 2));
+    const uint32_t rpw = ms_rpw(S);
+    r.m = m;
+    r.tile = gt - t0;
+    r.row0 = r.tile * rpw;
+    const bool last = gt == t1 - 1;
+    r.nrows = last ? rows - r.row0 : rpw;
+    r.lanes = last ? r.nrows * ms_upr(S) : ms_lpt(S);
+    r.base = w + (uint64_t)r.tile * ms_tb(S);
+    return r;
+}
+
+// Folds the n4 float4 at p (LDS) in order with f, B float4 per batch; the
+// next batch is read before the current one is folded, so LDS latency is paid
+// once per batch pair rather than once per read.
+template <int B, typename F>
+__device__ __forceinline__ void lds_fold4(const float4 *p, uint32_t n4, F &&f) {
+    const uint32_t nb = n4 / B;
+    if (nb) {
+        float4 cur[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) cur[u] = p[u];
+        for (uint32_t k = 0; k < nb; k++) {
+            float4 nxt[B];
+            if (k + 1 < nb) {
+#pragma unroll
+                for (int u = 0; u < B; u++) nxt[u] = p[(k + 1) * B + u];
+            }
+#pragma unroll
+            for (int u = 0; u < B; u++) f(cur[u]);
+#pragma unroll
+            for (int u = 0; u < B; u++) cur[u] = nxt[u];
+        }
+    }
+    for (uint32_t i = nb * B; i < n4; i++) f(p[i]);
+}
+
+// Float4 reads in flight per row sum: deep batches shorten a single
+// wavefront's chain (the persistent kernel, one wavefront per SIMD); the
+// standalone GEMVs keep registers low so more wavefronts share a SIMD.
+#ifndef PI_CHAIN_BATCH
+#define PI_CHAIN_BATCH 1
+#endif
+
 // Sums n terms of the strip at p strictly left to right, starting from 0.
 __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
     float acc = 0.0f;
     if ((n & 3u) == 0) {
-        const float4 *p4 = reinterpret_cast<const float4 *>(p);
-        for (uint32_t i = 0; i < n / 4; i++) {
-            const float4 v = p4[i];
+        lds_fold4<PI_CHAIN_BATCH>(reinterpret_cast<const float4 *>(p), n / 4, [&](const float4 &v) {
             acc += v.x;
             acc += v.y;
             acc += v.z;
             acc += v.w;
-        }
+        });
     } else {
         for (uint32_t i = 0; i < n; i++) acc += p[i];
     }
@@ -333,8 +434,8 @@ __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
 // the lane owning it calls out(m, row, value) with value = 0 + sum of terms.
 // Weights of the next tile are requested before the current tile is used
 // (two named buffers, so both stay in registers).
-template <uint32_t T, int G, typename Out>
-__device__ __forceinline__ void consume_tile(const MatSet &S, const Slice<T, G> &A, const Unit<T, G> &U,
+template <uint32_t T, int G, typename SS, typename Out>
+__device__ __forceinline__ void consume_tile(const SS &S, const Slice<T, G> &A, const Unit<T, G> &U,
                                              const TileRef &R, float *strip, Out &out) {
     constexpr int TPU = QT<T>::TPB * G;
     const uint32_t lane = threadIdx.x & 63u;
@@ -346,20 +447,20 @@ __device__ __forceinline__ void consume_tile(const MatSet &S, const Slice<T, G> 
         for (int t = 0; t < TPU; t++) strip[lane * TPU + t] = term[t];
     }
     wave_sync();
-    const uint32_t per_row = S.upr * TPU;
+    const uint32_t per_row = ms_upr(S) * TPU;
     if (lane < R.nrows) out(R.m, R.row0 + lane, 0.0f + chain_sum(strip + lane * per_row, per_row));
     wave_sync();
 }
 
-template <uint32_t T, int G, typename Out>
-__device__ __forceinline__ void run_tiles(const MatSet &S, const Slice<T, G> &A, uint32_t first, uint32_t stride,
-                                          float *strip, Out out) {
+// Runs the tiles gt = first, first + stride, ... of S on one wavefront, the
+// first of them already loaded into UA (tile reference RA).
+template <uint32_t T, int G, typename SS, typename Out>
+__device__ __forceinline__ void run_tiles_pre(const SS &S, const Slice<T, G> &A, Unit<T, G> UA, TileRef RA,
+                                              uint32_t first, uint32_t stride, float *strip, Out out) {
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t nt = S.tile0[S.n];
-    if (first >= nt) return;
-    Unit<T, G> UA, UB;
-    TileRef RA = tile_ref(S, first), RB;
-    UA.load(RA.base, RA.lanes, min(lane, RA.lanes - 1));
+    const uint32_t nt = ms_total(S);
+    Unit<T, G> UB;
+    TileRef RB;
     uint32_t gt = first;
     for (;;) {
         uint32_t gn = gt + stride;
@@ -367,17 +468,28 @@ __device__ __forceinline__ void run_tiles(const MatSet &S, const Slice<T, G> &A,
         // always issue the next load (the current tile again when there is none)
         RB = tile_ref(S, more ? gn : gt);
         UB.load(RB.base, RB.lanes, min(lane, RB.lanes - 1));
-        consume_tile<T, G>(S, A, UA, RA, strip, out);
+        consume_tile<T, G, SS>(S, A, UA, RA, strip, out);
         if (!more) break;
         gt = gn;
         gn = gt + stride;
         more = gn < nt;
         RA = tile_ref(S, more ? gn : gt);
         UA.load(RA.base, RA.lanes, min(lane, RA.lanes - 1));
-        consume_tile<T, G>(S, A, UB, RB, strip, out);
+        consume_tile<T, G, SS>(S, A, UB, RB, strip, out);
         if (!more) break;
         gt = gn;
     }
+}
+
+template <uint32_t T, int G, typename SS, typename Out>
+__device__ __forceinline__ void run_tiles(const SS &S, const Slice<T, G> &A, uint32_t first, uint32_t stride,
+                                          float *strip, Out out) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (first >= ms_total(S)) return;
+    Unit<T, G> UA;
+    const TileRef RA = tile_ref(S, first);
+    UA.load(RA.base, RA.lanes, min(lane, RA.lanes - 1));
+    run_tiles_pre<T, G, SS>(S, A, UA, RA, first, stride, strip, out);
 }
 
 // Integer block sums of the tiles (test hook): per 32 elements, or per 16 for
@@ -387,7 +499,7 @@ __device__ __forceinline__ void run_tiles_sums(const MatSet &S, const Slice<T, G
                                                uint32_t stride, int32_t *sums) {
     constexpr int TPU = QT<T>::TPB * G;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t nt = S.tile0[S.n];
+    const uint32_t nt = ms_total(S);
     for (uint32_t gt = first; gt < nt; gt += stride) {
         const TileRef R = tile_ref(S, gt);
         Unit<T, G> U;
@@ -402,6 +514,50 @@ __device__ __forceinline__ void run_tiles_sums(const MatSet &S, const Slice<T, G
             for (int t = 0; t < TPU; t++) dst[t] = isum[t];
         }
     }
+}
+
+// One element of a token_embd row in its native layout (dequant_row,
+// quant.rs:102-359, for the types with kernels).
+__device__ __forceinline__ float embed_elem(const uint8_t *row, uint32_t type, uint32_t e) {
+    float v = 0.0f;
+    if (type == PI_TYPE_F32) {
+        memcpy(&v, row + 4 * (uint64_t)e, 4);
+    } else if (type == PI_TYPE_Q4_K) {
+        const uint8_t *b = row + (uint64_t)(e / 256) * 144;
+        const uint32_t j = e % 256, g = j / 64, hi = (j % 64) >= 32, l = j % 32, is = 2 * g + hi;
+        const float dd = h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8)), dm = h2f((uint32_t)b[2] | ((uint32_t)b[3] << 8));
+        const uint8_t *sc = b + 4;
+        uint32_t s, m;
+        if (is < 4) {
+            s = sc[is] & 63u;
+            m = sc[is + 4] & 63u;
+        } else {
+            s = (sc[is + 4] & 0xFu) | ((sc[is - 4] >> 6) << 4);
+            m = (sc[is + 4] >> 4) | ((sc[is] >> 6) << 4);
+        }
+        const uint32_t qv = hi ? (b[16 + g * 32 + l] >> 4) : (b[16 + g * 32 + l] & 0xFu);
+        const float d1 = dd * (float)s, m1 = dm * (float)m;
+        v = d1 * (float)qv - m1;
+    } else if (type == PI_TYPE_Q6_K) {
+        const uint8_t *b = row + (uint64_t)(e / 256) * 210;
+        const uint32_t j = e % 256, hf = j / 128, r = j % 128, s4 = r / 32, l = r % 32;
+        uint32_t qlv = b[hf * 64 + l + (s4 & 1u) * 32];
+        qlv = (s4 >= 2) ? (qlv >> 4) : (qlv & 0xFu);
+        const uint32_t qhv = (b[128 + hf * 32 + l] >> (2 * s4)) & 3u;
+        const int qq = (int)(qlv | (qhv << 4)) - 32;
+        const float dd = h2f((uint32_t)b[208] | ((uint32_t)b[209] << 8));
+        const float scv = (float)(int8_t)b[192 + hf * 8 + l / 16 + 2 * s4];
+        v = dd * scv * (float)qq;
+    } else if (type == PI_TYPE_Q4_0) {
+        const uint8_t *b = row + (uint64_t)(e / 32) * 18;
+        const uint32_t j = e % 32;
+        const uint32_t qv = j < 16 ? (b[2 + j] & 0xFu) : (b[2 + j - 16] >> 4);
+        v = ((float)qv - 8.0f) * h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    } else if (type == PI_TYPE_Q8_0) {
+        const uint8_t *b = row + (uint64_t)(e / 32) * 34;
+        v = (float)(int8_t)b[2 + e % 32] * h2f((uint32_t)b[0] | ((uint32_t)b[1] << 8));
+    }
+    return v;
 }
 
 }  // namespace pig

@@ -1,0 +1,1037 @@
+// Persistent decode kernel for gfx950: one cooperative launch = one token
+// through every layer (model.rs:857-1170), one workgroup of 4 wavefronts per
+// CU, all workgroups resident.
+//
+// Stages of a layer and who runs them:
+//   S1  every workgroup: x -> RMSNorm + Q8 into LDS; Q/K/V tiles    -> q, k, v
+//   S2  one workgroup per head: RoPE, KV write, attention, Q8       -> att
+//   S3  every workgroup: att -> LDS; attn_output tiles, x + proj    -> xb
+//   S4  every workgroup: xb -> RMSNorm + Q8; gate/up tile pairs,
+//       SwiGLU                                                       -> h
+//   S5  every workgroup: h -> Q8; ffn_down tiles, xb + proj          -> xo
+// then, with the head: xo -> output norm + Q8; head tiles -> logits and a
+// per-workgroup (max, first index) pair; workgroup 0 reduces the pairs to the
+// greedy id (sampler.rs:26-36).
+//
+// Hand-off: every output element is one 64-bit word (value bits | epoch
+// << 32) stored with a device-scope atomic store; a consumer re-reads a word
+// until it carries the launch's epoch.  Each layer has its own words, so a
+// word is written once per launch and no stage can overwrite data another
+// workgroup still reads.  Dependencies only point to earlier stages and every
+// workgroup runs the stages in order, so with all workgroups resident
+// (cooperative launch) every wait ends; each wait is also bounded and raises
+// the abort flag when exceeded, after which every workgroup leaves.
+//
+// Each stage requests its first weight tile before it waits for its input,
+// so the HBM latency of the weights overlaps the hand-off.  The GEMV core,
+// Q8 rule and float orders are those of pi_gemv.h / pi_decode.hip, so the
+// results are bit-identical to the CPU path.
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#define PI_CHAIN_BATCH 6
+#include "pi_mega.h"
+
+using namespace pig;
+
+namespace {
+
+constexpr uint32_t MT = 256;           // threads per workgroup
+constexpr uint32_t MW = MT / 64;       // wavefronts per workgroup
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t kChunk = 64;        // attention positions per product chunk
+constexpr uint32_t kChunkPad = 68;     // floats per dimension row of a chunk (16-byte aligned)
+constexpr uint32_t kRedFloats = 512;   // small LDS scratch
+constexpr uint32_t kStripFloats = MW * 64 * 16;
+
+__host__ __device__ constexpr uint32_t xt_stride(uint32_t ne) { return ne / 8 + 4; }
+__host__ __device__ constexpr uint32_t align16(uint32_t b) { return (b + 15u) & ~15u; }
+__host__ __device__ constexpr uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// ---------------------------------------------------------------------------
+// flag-tagged words
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t ll_get(const uint64_t *p) {
+    return __hip_atomic_load(gst(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ll_put(uint64_t *p, uint32_t bits, uint32_t epoch) {
+    __hip_atomic_store(gst(p), ((uint64_t)epoch << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool aborted(const int32_t *f) {
+    return __hip_atomic_load(gst(const_cast<int32_t *>(f)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+__device__ __forceinline__ void raise_abort(int32_t *f) {
+    __hip_atomic_store(gst(f), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Re-reads p until it carries `epoch` (w: the last value read).  False when
+// the spin bound is exceeded or another workgroup raised the abort flag.
+__device__ __forceinline__ bool ll_wait(const uint64_t *p, uint32_t epoch, uint64_t &w, const int32_t *abort_flag) {
+    uint32_t it = 0;
+    while ((uint32_t)(w >> 32) != epoch) {
+        ++it;
+        if ((it & 63u) == 0 && (it > kSpinLimit || aborted(abort_flag))) return false;
+        __builtin_amdgcn_s_sleep(1);
+        w = ll_get(p);
+    }
+    return true;
+}
+
+// Every thread of the workgroup polls words tid, tid + MT, ... (U of them at
+// a time).  Each round re-reads every word still missing, so words that
+// arrive one after another cost one round trip together, not one each.
+// dst(i, bits) stores word i.
+template <int U, typename Dst>
+__device__ __forceinline__ bool wg_poll(const uint64_t *src, uint32_t n, uint32_t epoch, const int32_t *abort_flag,
+                                        Dst dst) {
+    static_assert(U <= 32, "pending mask is 32 bits");
+    for (uint32_t i0 = threadIdx.x; i0 < n; i0 += MT * U) {
+        uint64_t w[U];
+        uint32_t pending = 0;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const uint32_t i = i0 + u * MT;
+            if (i < n) {
+                w[u] = ll_get(src + i);
+                pending |= 1u << u;
+            }
+        }
+        for (uint32_t it = 0;; ++it) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                if (((pending >> u) & 1u) && (uint32_t)(w[u] >> 32) == epoch) {
+                    dst(i0 + u * MT, (uint32_t)w[u]);
+                    pending &= ~(1u << u);
+                }
+            }
+            if (!pending) break;
+            if ((it & 63u) == 63u && (it > kSpinLimit || aborted(abort_flag))) return false;
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if ((pending >> u) & 1u) w[u] = ll_get(src + i0 + u * MT);
+        }
+    }
+    return true;
+}
+
+// Per-launch scalars handed to every stage.
+struct Run {
+    int32_t pos;
+    uint32_t epoch;
+    bool neon;    // batch-1 float orders (else the multi-token chunk orders)
+    bool detail;  // record the in-stage trace points (middle layer)
+};
+
+// Scalar fields of the launch arguments, read once with scalar loads.
+struct Cfg {
+    const pi_mega_args *args;
+    const pi_mega_layer *layers;
+    uint32_t n_layer, ne, n_ff, n_head, n_kv, half, n_ctx, etype, t_head;
+    float eps, scale;
+    const float *cos_tab, *sin_tab, *out_norm;
+    const uint8_t *embd;
+    uint64_t erow_bytes;
+    float *logits;
+    uint64_t *part, *trace;
+    uint32_t *tok_state;
+    int32_t *abort_flag;
+};
+
+__device__ __forceinline__ Cfg load_cfg(const pi_mega_args *ap) {
+    Cfg c;
+    c.args = ap;
+    c.layers = cload(&ap->layers);
+    c.n_layer = cload(&ap->n_layer); c.ne = cload(&ap->ne); c.n_ff = cload(&ap->n_ff);
+    c.n_head = cload(&ap->n_head); c.n_kv = cload(&ap->n_kv); c.half = cload(&ap->half);
+    c.n_ctx = cload(&ap->n_ctx); c.etype = cload(&ap->etype); c.t_head = cload(&ap->t_head);
+    c.eps = cload(&ap->eps); c.scale = cload(&ap->scale);
+    c.cos_tab = cload(&ap->cos_tab); c.sin_tab = cload(&ap->sin_tab); c.out_norm = cload(&ap->out_norm);
+    c.embd = cload(&ap->embd); c.erow_bytes = cload(&ap->erow_bytes);
+    c.logits = cload(&ap->logits); c.part = cload(&ap->part); c.trace = cload(&ap->trace);
+    c.tok_state = cload(&ap->tok_state); c.abort_flag = cload(&ap->abort_flag);
+    return c;
+}
+
+// Workgroup barrier that orders LDS only.  Every cross-wavefront exchange in
+// this kernel goes through LDS (global hand-offs carry their own epoch), so
+// the barriers never need to wait for in-flight global loads or stores, such
+// as a weight tile requested before a stage's input has arrived.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Workgroup OR of a predicate: wavefront ballots through 4 LDS words.
+__device__ __forceinline__ bool wg_any(bool pred, int32_t *vote) {
+    const bool any = __ballot(pred) != 0;
+    lds_barrier();  // earlier readers of the words are done
+    if ((threadIdx.x & 63u) == 0) vote[threadIdx.x >> 6] = any ? 1 : 0;
+    lds_barrier();
+    return (vote[0] | vote[1] | vote[2] | vote[3]) != 0;
+}
+
+// s_waitcnt vmcnt(0): every global load of this wavefront has landed.  Used
+// where that is already true (after a completed poll) so the compiler stops
+// guarding each following LDS access with a wait for in-flight loads.
+__device__ __forceinline__ void vm_drain() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+__device__ __forceinline__ float comp4(const float4 &v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+// ---------------------------------------------------------------------------
+// LDS of a workgroup
+// ---------------------------------------------------------------------------
+struct QAct {        // Q8 activation of k elements (quant_int.rs:3-14)
+    uint32_t *qw;    // k/4 words of quants
+    float *d;        // k/32 block scales
+    int32_t *s;      // k/32 block sums
+};
+
+struct Lds {
+    float *xt;       // residual x, transposed: x[8j + c] at xt[c * XT + j]
+    uint32_t XT;
+    QAct act;        // Q8 activation of the stage input
+    float *hb;       // h staging, embedding row bytes, attention products
+    float *strip;    // this wavefront's term strip (64 * 16 floats)
+    float *red;      // scratch
+    float *sc;       // attention scores (n_ctx)
+    int32_t *vote;   // wg_any words
+};
+
+struct LdsPlan {
+    uint32_t xt, act, hb, strips, red, sc, total;
+};
+
+__host__ __device__ inline LdsPlan lds_plan(uint32_t ne, uint32_t n_ff, uint32_t n_ctx) {
+    LdsPlan p{};
+    const uint32_t kmax = umax(ne, n_ff);
+    p.xt = 0;
+    p.act = p.xt + align16(8u * xt_stride(ne) * 4u);
+    p.hb = p.act + align16(kmax + kmax / 32u * 8u);
+    p.strips = p.hb + align16(umax(umax(n_ff, ne) * 4u, 2u * kChunk * kChunkPad * 4u));
+    p.red = p.strips + kStripFloats * 4u;
+    p.sc = p.red + kRedFloats * 4u;
+    p.total = p.sc + align16(n_ctx * 4u);
+    return p;
+}
+
+__device__ __forceinline__ Lds carve(unsigned char *smem, uint32_t ne, uint32_t n_ff, uint32_t n_ctx) {
+    const LdsPlan p = lds_plan(ne, n_ff, n_ctx);
+    Lds L;
+    L.xt = reinterpret_cast<float *>(smem + p.xt);
+    L.XT = xt_stride(ne);
+    L.act.qw = reinterpret_cast<uint32_t *>(smem + p.act);
+    L.hb = reinterpret_cast<float *>(smem + p.hb);
+    L.strip = reinterpret_cast<float *>(smem + p.strips) + (threadIdx.x >> 6) * 64 * 16;
+    L.red = reinterpret_cast<float *>(smem + p.red);
+    L.vote = reinterpret_cast<int32_t *>(L.red + kRedFloats - 8);
+    L.sc = reinterpret_cast<float *>(smem + p.sc);
+    return L;
+}
+__device__ __forceinline__ void set_act_k(Lds &L, uint32_t k) {
+    L.act.d = reinterpret_cast<float *>(reinterpret_cast<unsigned char *>(L.act.qw) + k);
+    L.act.s = reinterpret_cast<int32_t *>(reinterpret_cast<unsigned char *>(L.act.qw) + k + (k / 32) * 4);
+}
+__device__ __forceinline__ float xt_at(const Lds &L, uint32_t i) { return L.xt[(i & 7u) * L.XT + (i >> 3)]; }
+__device__ __forceinline__ void xt_set(const Lds &L, uint32_t i, float v) { L.xt[(i & 7u) * L.XT + (i >> 3)] = v; }
+
+__device__ __forceinline__ void trace_mark(const Cfg &a, uint32_t slot) {
+    if (a.trace && threadIdx.x == 0)
+        gst(a.trace)[(uint64_t)blockIdx.x * pi_mega_trace_slots(a.n_layer) + slot] = __builtin_amdgcn_s_memrealtime();
+}
+// Point k (< 16) inside a stage of the middle layer.
+__device__ __forceinline__ void trace_detail(const Cfg &a, const Run &r, uint32_t k) {
+    if (r.detail) trace_mark(a, 3 + 5 * a.n_layer + k);
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm (model.rs:777-823) of the x held in xt, then Q8Act::prepare
+// (quant_int.rs:17-56) into L.act.  NEON: simd::f32_sum_sq (simd.rs:45-64):
+// eight FMA chains over the stride-8 elements, lane-wise acc0 + acc1, then
+// (t0 + t1) + (t2 + t3); else the scalar loop of a multi-token batch.
+// out = (x * s) * w.  wr: this thread's 32 norm weights (threads < ne/32).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, const float4 (&wr)[8], bool neon) {
+    const uint32_t tid = threadIdx.x;
+    const uint32_t n4 = ne / 32;  // float4 per transposed row (a multiple of 4: ne % 128 == 0)
+    vm_drain();
+    if (neon) {
+        if (tid < 8) {
+            const float4 *row = reinterpret_cast<const float4 *>(L.xt + tid * L.XT);
+            float acc = 0.0f;
+            lds_fold4<6>(row, n4, [&](const float4 &v) {
+                acc = __builtin_fmaf(v.x, v.x, acc);
+                acc = __builtin_fmaf(v.y, v.y, acc);
+                acc = __builtin_fmaf(v.z, v.z, acc);
+                acc = __builtin_fmaf(v.w, v.w, acc);
+            });
+            L.red[tid] = acc;
+        }
+        wave_sync();
+        if (tid == 0) {
+            const float t0 = L.red[0] + L.red[4], t1 = L.red[1] + L.red[5], t2 = L.red[2] + L.red[6],
+                        t3 = L.red[3] + L.red[7];
+            const float ss = (t0 + t1) + (t2 + t3);
+            L.red[8] = 1.0f / sqrtf(ss / (float)ne + eps);
+        }
+    } else {
+        if (tid == 0) {
+            float ss = 0.0f;
+            for (uint32_t j = 0; j < n4; j++) {
+                float4 r[8];
+#pragma unroll
+                for (int c = 0; c < 8; c++) r[c] = reinterpret_cast<const float4 *>(L.xt + c * L.XT)[j];
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        const float v = comp4(r[c], q);
+                        ss += v * v;
+                    }
+            }
+            L.red[8] = 1.0f / sqrtf(ss / (float)ne + eps);
+        }
+    }
+    lds_barrier();
+    const float s = L.red[8];
+    if (tid < ne / 32) {
+        float v[32];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+            const float4 t = reinterpret_cast<const float4 *>(L.xt + c * L.XT)[tid];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int e = 8 * q + c;
+                v[e] = comp4(t, q) * s * comp4(wr[e / 4], e % 4);
+            }
+        }
+        q8_lane(v, L.act.qw + 8 * tid, L.act.d + tid, L.act.s + tid);
+    }
+    lds_barrier();
+}
+
+__device__ __forceinline__ void load_norm_w(const float *w, uint32_t ne, float4 (&wr)[8]) {
+    if (threadIdx.x < ne / 32) {
+        const PI_GLOBAL float4 *w4 = gld(reinterpret_cast<const float4 *>(w + 32 * threadIdx.x));
+#pragma unroll
+        for (int j = 0; j < 8; j++) wr[j] = w4[j];
+    }
+}
+
+// Polls n_embd residual words into xt.
+__device__ __forceinline__ bool poll_x(const Lds &L, const uint64_t *src, uint32_t ne, uint32_t epoch,
+                                       const int32_t *abort_flag) {
+    return wg_poll<9>(src, ne, epoch, abort_flag, [&](uint32_t i, uint32_t bits) { xt_set(L, i, __uint_as_float(bits)); });
+}
+
+// ---------------------------------------------------------------------------
+// GEMV tiles of one matrix set on a Q8 activation in LDS.  A wavefront owns
+// tiles first, first + stride, ...; its first P tiles are requested into a
+// register ring before the stage waits for its input (prefetch_ring), and
+// after tile i is consumed, tile i + P is requested into its slot.
+// ---------------------------------------------------------------------------
+template <uint32_t T, int G, int P, typename SS>
+__device__ __forceinline__ void prefetch_ring(const SS &S, uint32_t first, uint32_t stride, Unit<T, G> (&U)[P],
+                                              TileRef (&R)[P]) {
+    const uint32_t nt = ms_total(S), lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        const uint32_t gt = first + (uint32_t)k * stride;
+        if (gt < nt) {
+            R[k] = tile_ref(S, gt);
+            U[k].load(R[k].base, R[k].lanes, min(lane, R[k].lanes - 1));
+        }
+    }
+}
+
+template <uint32_t T, int G, int P, typename SS, typename Out>
+__device__ __forceinline__ void gemv_ring(const SS &S, const Lds &L, Unit<T, G> (&U)[P], TileRef (&R)[P],
+                                          uint32_t first, uint32_t stride, Out out) {
+    const uint32_t lane = threadIdx.x & 63u, nt = ms_total(S);
+    if (first >= nt) return;
+    Slice<T, G> SL;
+    SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, lane % ms_upr(S));
+    uint32_t gt = first;
+    for (;;) {
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            if (gt >= nt) return;
+            consume_tile<T, G, SS>(S, SL, U[k], R[k], L.strip, out);
+            const uint32_t gn = gt + (uint32_t)P * stride;
+            if (gn < nt) {
+                R[k] = tile_ref(S, gn);
+                U[k].load(R[k].base, R[k].lanes, min(lane, R[k].lanes - 1));
+            }
+            gt += stride;
+        }
+    }
+}
+
+// Calls f(integral_constant<T>, integral_constant<G>) for the runtime type/g.
+template <typename F>
+__device__ __forceinline__ void with_kq(uint32_t t, F &&f) {
+    if (t == PI_TYPE_Q6_K) f(std::integral_constant<uint32_t, PI_TYPE_Q6_K>{}, std::integral_constant<int, 1>{});
+    else f(std::integral_constant<uint32_t, PI_TYPE_Q4_K>{}, std::integral_constant<int, 1>{});
+}
+template <typename F>
+__device__ __forceinline__ void with_any(uint32_t t, uint32_t g, F &&f) {
+    using I = std::integral_constant<int, 1>;
+    switch (t) {
+    case PI_TYPE_Q4_K: f(std::integral_constant<uint32_t, PI_TYPE_Q4_K>{}, I{}); return;
+    case PI_TYPE_Q6_K: f(std::integral_constant<uint32_t, PI_TYPE_Q6_K>{}, I{}); return;
+    default: break;
+    }
+    auto by_g = [&](auto T) {
+        switch (g) {
+        case 1: f(T, std::integral_constant<int, 1>{}); return;
+        case 2: f(T, std::integral_constant<int, 2>{}); return;
+        case 3: f(T, std::integral_constant<int, 3>{}); return;
+        case 4: f(T, std::integral_constant<int, 4>{}); return;
+        case 6: f(T, std::integral_constant<int, 6>{}); return;
+        default: f(T, std::integral_constant<int, 8>{}); return;
+        }
+    };
+    if (t == PI_TYPE_Q4_0) by_g(std::integral_constant<uint32_t, PI_TYPE_Q4_0>{});
+    else by_g(std::integral_constant<uint32_t, PI_TYPE_Q8_0>{});
+}
+
+#define PI_POLL_OR_LEAVE(expr)                                   \
+    do {                                                         \
+        if (wg_any(!(expr), L.vote)) {                           \
+            if (threadIdx.x == 0) raise_abort(a.abort_flag);     \
+            return false;                                        \
+        }                                                        \
+    } while (0)
+
+// ---------------------------------------------------------------------------
+// S1: RMSNorm + Q8 + Q/K/V.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, const uint64_t *xin,
+                          uint32_t gw, uint32_t nw) {
+    Lds L = Lc;
+    set_act_k(L, a.ne);
+    bool ok = true;
+    const SetRef SA{&Yp->qkv}, SB{&Yp->vb};
+    const uint32_t t_qkv = cload(&Yp->t_qkv), t_vb = cload(&Yp->t_vb);
+    const float *attn_norm = cload(&Yp->attn_norm);
+    uint64_t *oq = cload(&Yp->q), *okk = cload(&Yp->k), *ov = cload(&Yp->v);
+    const uint32_t ntA = ms_total(SA);
+    const uint32_t ntB = ms_n(SB) ? ms_total(SB) : 0u;
+    // segment B continues the wavefront numbering after segment A
+    const uint32_t firstB = (gw + nw - ntA % nw) % nw;
+    with_kq(t_qkv, [&](auto TA_, auto) {
+        with_kq(ntB ? t_vb : t_qkv, [&](auto TB_, auto) {
+            constexpr uint32_t TA = decltype(TA_)::value, TB = decltype(TB_)::value;
+            Unit<TA, 1> UA[1];
+            Unit<TB, 1> UB[1];
+            TileRef RA[1], RB[1];
+            const bool b_first = gw >= ntA && firstB < ntB;   // B is this wavefront's first work
+            if (b_first) prefetch_ring<TB, 1, 1>(SB, firstB, nw, UB, RB);
+            else prefetch_ring<TA, 1, 1>(SA, gw, nw, UA, RA);
+            float4 wr[8];
+            load_norm_w(attn_norm, a.ne, wr);
+            lds_barrier();
+            if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);
+            if (wg_any(!ok, L.vote)) { ok = false; return; }
+            trace_detail(a, r, 0);
+            norm_q8(L, a.ne, a.eps, wr, r.neon);
+            trace_detail(a, r, 1);
+            auto outA = [&](uint32_t m, uint32_t row, float v) {
+                uint64_t *o = m == 0 ? oq : (m == 1 ? okk : ov);
+                ll_put(o + row, __float_as_uint(v), r.epoch);
+            };
+            auto outB = [&](uint32_t, uint32_t row, float v) { ll_put(ov + row, __float_as_uint(v), r.epoch); };
+            if (b_first) {
+                gemv_ring<TB, 1, 1>(SB, L, UB, RB, firstB, nw, outB);
+            } else {
+                gemv_ring<TA, 1, 1>(SA, L, UA, RA, gw, nw, outA);
+                if (firstB < ntB) {
+                    prefetch_ring<TB, 1, 1>(SB, firstB, nw, UB, RB);
+                    gemv_ring<TB, 1, 1>(SB, L, UB, RB, firstB, nw, outB);
+                }
+            }
+            trace_detail(a, r, 2);
+        });
+    });
+    if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
+    return ok;
+}
+
+// ---------------------------------------------------------------------------
+// S2: attention of head h for the token at r.pos (model.rs:953-1087).
+// RoPE of q and k over adjacent pairs, K/V row write (first head of a KV
+// group), scores q.k_p * scale for p = 0..pos (NEON: simd::f32_dot's two
+// 4-lane accumulators; else the scalar loop), max, e_p = exp(s_p - max),
+// sum over p in order, o[d] = sum over p in order of e_p * v_p[d] skipping
+// e_p == 0 (f32_axpy: product rounded, then added), o * (1/sum), Q8 of o.
+// Wavefronts 1-3 form the products of the next chunk of positions while
+// wavefront 0 (lane = dimension) adds the current chunk in order; wavefront
+// 3 also keeps the running sum of e_p.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &L, uint32_t h) {
+    constexpr uint32_t DH = 64;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
+    const uint32_t group = a.n_head / a.n_kv, kvh = h / group;
+    const int pos = r.pos;
+    const uint32_t n = (uint32_t)pos + 1;
+    const uint64_t *yq = cload(&Yp->q), *yk = cload(&Yp->k), *yv = cload(&Yp->v);
+    uint64_t *yatt = cload(&Yp->att);
+    float *ykc = cload(&Yp->kc), *yvc = cload(&Yp->vc);
+    float *qs = L.red, *kcur = L.red + 64, *vcur = L.red + 128, *misc = L.red + 192;
+    // inputs: q of head h, k and v of its KV head
+    bool ok = true;
+    if (tid < 3 * DH) {
+        const uint32_t part = tid / DH, d = tid % DH;
+        const uint64_t *src = part == 0 ? yq + h * DH + d : (part == 1 ? yk + kvh * DH + d : yv + kvh * DH + d);
+        uint64_t w = ll_get(src);
+        ok = ll_wait(src, r.epoch, w, a.abort_flag);
+        L.red[tid] = __uint_as_float((uint32_t)w);
+    }
+    PI_POLL_OR_LEAVE(ok);
+    trace_detail(a, r, 3);
+    const PI_GLOBAL float *cb = gld(a.cos_tab + (uint64_t)pos * a.half), *sb = gld(a.sin_tab + (uint64_t)pos * a.half);
+    if (tid < DH / 2 && tid < a.half) {
+        const uint32_t i = tid;
+        const float c = cb[i], s = sb[i];
+        const float x0 = qs[2 * i], x1 = qs[2 * i + 1], y0 = kcur[2 * i], y1 = kcur[2 * i + 1];
+        qs[2 * i] = x0 * c - x1 * s;
+        qs[2 * i + 1] = x0 * s + x1 * c;
+        kcur[2 * i] = y0 * c - y1 * s;
+        kcur[2 * i + 1] = y0 * s + y1 * c;
+    }
+    lds_barrier();
+    float *kbase = ykc + (uint64_t)kvh * a.n_ctx * DH;
+    float *vbase = yvc + (uint64_t)kvh * a.n_ctx * DH;
+    if (h % group == 0 && tid < DH) {
+        gst(kbase)[(uint64_t)pos * DH + tid] = kcur[tid];
+        gst(vbase)[(uint64_t)pos * DH + tid] = vcur[tid];
+    }
+    // scores; the K row of the next position of this thread is requested
+    // before the current one is used
+    float mx = -INFINITY;
+    const float4 *q4 = reinterpret_cast<const float4 *>(qs);
+    // Every K row comes from HBM (the row of the current position may not be
+    // visible yet and is recomputed from LDS below), so loads never share a
+    // destination register with an LDS read.
+    auto load_k = [&](uint32_t p, float4 (&kr)[16]) {
+        const PI_GLOBAL float4 *src = gld(reinterpret_cast<const float4 *>(kbase + (uint64_t)p * DH));
+#pragma unroll
+        for (int i = 0; i < 16; i++) kr[i] = src[i];
+    };
+    auto score = [&](const float4 (&kr)[16]) {
+        float s;
+        if (r.neon) {
+            float a0[4] = {0.f, 0.f, 0.f, 0.f}, a1[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 qa = q4[2 * i], qb = q4[2 * i + 1], ka = kr[2 * i], kb = kr[2 * i + 1];
+                a0[0] = a0[0] + qa.x * ka.x; a0[1] = a0[1] + qa.y * ka.y;
+                a0[2] = a0[2] + qa.z * ka.z; a0[3] = a0[3] + qa.w * ka.w;
+                a1[0] = a1[0] + qb.x * kb.x; a1[1] = a1[1] + qb.y * kb.y;
+                a1[2] = a1[2] + qb.z * kb.z; a1[3] = a1[3] + qb.w * kb.w;
+            }
+            s = (a0[0] + a0[1]) + (a0[2] + a0[3]);
+            s += (a1[0] + a1[1]) + (a1[2] + a1[3]);
+        } else {
+            s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const float4 qa = q4[i], ka = kr[i];
+                s += qa.x * ka.x;
+                s += qa.y * ka.y;
+                s += qa.z * ka.z;
+                s += qa.w * ka.w;
+            }
+        }
+        return s * a.scale;
+    };
+    float4 kr[16];
+    if (tid < n) load_k(tid, kr);
+    for (uint32_t p = tid; p < n; p += MT) {
+        float4 kn[16];
+        if (p + MT < n) load_k(p + MT, kn);
+        const float s = score(kr);
+        if (p != (uint32_t)pos) {
+            L.sc[p] = s;
+            mx = fmaxf(mx, s);
+        }
+#pragma unroll
+        for (int i = 0; i < 16; i++) kr[i] = kn[i];
+    }
+    vm_drain();
+    if (tid == (uint32_t)pos % MT) {
+        float4 kc4[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) kc4[i] = reinterpret_cast<const float4 *>(kcur)[i];
+        const float s = score(kc4);
+        L.sc[pos] = s;
+        mx = fmaxf(mx, s);
+    }
+#pragma unroll
+    for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) misc[wave] = mx;
+    lds_barrier();
+    mx = fmaxf(fmaxf(misc[0], misc[1]), fmaxf(misc[2], misc[3]));
+    for (uint32_t p = tid; p < n; p += MT) L.sc[p] = pi_expf(L.sc[p] - mx);
+    lds_barrier();
+    trace_detail(a, r, 4);
+
+    // Products e_p * v_p[d] of chunk c go to buffer c & 1, laid out [d][p].
+    // A chunk is 16 groups of 4 positions; wavefronts 1-3 own groups w-1,
+    // w+2, ... (lane l: position 4g + l/16, dimensions 4(l%16)..+3, one
+    // 16-byte load) and keep the V rows of the next kDepth chunks in flight
+    // in registers; wavefront 0 adds chunk c - 1 in order while chunk c is
+    // being formed.  V rows always come from HBM (rows past the end re-read
+    // row n-1); the current position's row is taken from LDS.
+    constexpr int GPW = (kChunk / 4 + MW - 2) / (MW - 1);   // groups per product wavefront
+    constexpr int kDepth = 4;
+    const uint32_t nchunk = (n + kChunk - 1) / kChunk;
+    const uint32_t d0 = 4 * (lane % 16), sub = lane / 16;
+    const float4 vme = reinterpret_cast<const float4 *>(vcur)[lane % 16];
+    float4 vr[kDepth][GPW];
+    auto load_v = [&](uint32_t c, float4 (&v)[GPW]) {
+#pragma unroll
+        for (int i = 0; i < GPW; i++) {
+            const uint32_t g = (wave - 1) + (MW - 1) * i;
+            const uint32_t p = min(c * kChunk + 4 * g + sub, n - 1);
+            v[i] = gld(reinterpret_cast<const float4 *>(vbase + (uint64_t)p * DH))[lane % 16];
+        }
+    };
+    auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
+        float *buf = L.hb + (c & 1u) * kChunk * kChunkPad;
+#pragma unroll
+        for (int i = 0; i < GPW; i++) {
+            const uint32_t g = (wave - 1) + (MW - 1) * i, rr = 4 * g + sub, p = c * kChunk + rr;
+            if (g < kChunk / 4 && p < n) {
+                const float e = L.sc[p];
+                const float4 vv = p == (uint32_t)pos ? vme : v[i];
+                buf[(d0 + 0) * kChunkPad + rr] = (e != 0.0f) ? e * vv.x : 0.0f;
+                buf[(d0 + 1) * kChunkPad + rr] = (e != 0.0f) ? e * vv.y : 0.0f;
+                buf[(d0 + 2) * kChunkPad + rr] = (e != 0.0f) ? e * vv.z : 0.0f;
+                buf[(d0 + 3) * kChunkPad + rr] = (e != 0.0f) ? e * vv.w : 0.0f;
+            }
+        }
+    };
+    if (wave != 0) {
+#pragma unroll
+        for (int k = 0; k < kDepth; k++)
+            if ((uint32_t)k < nchunk) load_v(k, vr[k]);
+    }
+    float acc = 0.0f, sum = 0.0f;
+    for (uint32_t c0 = 0; c0 <= nchunk; c0 += kDepth) {
+#pragma unroll
+        for (int k = 0; k < kDepth; k++) {
+            const uint32_t c = c0 + k;
+            if (c > nchunk) break;
+            if (wave != 0) {
+                if (c < nchunk) {
+                    store_products(c, vr[k]);
+                    if (c + kDepth < nchunk) load_v(c + kDepth, vr[k]);
+                    if (wave == MW - 1 && lane == 0) {
+                        const uint32_t p0 = c * kChunk, rows = min(kChunk, n - p0);
+                        if (rows == kChunk) {
+                            const float4 *e4 = reinterpret_cast<const float4 *>(L.sc + p0);
+#pragma unroll
+                            for (uint32_t q = 0; q < kChunk / 4; q += 4) {
+                                float4 t[4];
+#pragma unroll
+                                for (int u = 0; u < 4; u++) t[u] = e4[q + u];
+#pragma unroll
+                                for (int u = 0; u < 4; u++) {
+                                    sum += t[u].x;
+                                    sum += t[u].y;
+                                    sum += t[u].z;
+                                    sum += t[u].w;
+                                }
+                            }
+                        } else {
+                            for (uint32_t q = 0; q < rows; q++) sum += L.sc[p0 + q];
+                        }
+                    }
+                }
+            } else if (c >= 1) {
+                const uint32_t cc = c - 1, rows = min(kChunk, n - cc * kChunk);
+                const float *row = L.hb + (cc & 1u) * kChunk * kChunkPad + lane * kChunkPad;
+                if (rows == kChunk) {
+#pragma unroll
+                    for (uint32_t q = 0; q < kChunk; q += 16) {
+                        float4 t[4];
+#pragma unroll
+                        for (int u = 0; u < 4; u++) t[u] = reinterpret_cast<const float4 *>(row + q)[u];
+#pragma unroll
+                        for (int u = 0; u < 4; u++) {
+                            acc = acc + t[u].x;
+                            acc = acc + t[u].y;
+                            acc = acc + t[u].z;
+                            acc = acc + t[u].w;
+                        }
+                    }
+                } else {
+                    for (uint32_t q = 0; q < rows; q++) acc = acc + row[q];
+                }
+            }
+            lds_barrier();
+        }
+    }
+    if (wave == MW - 1 && lane == 0) misc[8] = sum;
+    lds_barrier();
+    trace_detail(a, r, 5);
+    if (wave == 0) {
+        const float tot = misc[8];
+        const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+        const float o = acc * inv;
+        int8_t *qst = reinterpret_cast<int8_t *>(misc + 16);     // 64 quants
+        float *dst = misc + 32;                                  // 2 scales
+        int32_t *sst = reinterpret_cast<int32_t *>(misc + 34);   // 2 sums
+        q8_block32(o, (int)(lane % 32), qst + (lane / 32) * 32, dst + lane / 32, sst + lane / 32, true);
+        wave_sync();
+        // att words: quants (16 per head), then qdim/32 scales, then qdim/32 sums
+        const uint32_t qdim = a.n_head * DH;
+        if (lane < 16) ll_put(yatt + h * 16 + lane, reinterpret_cast<const uint32_t *>(qst)[lane], r.epoch);
+        else if (lane < 18) ll_put(yatt + qdim / 4 + h * 2 + (lane - 16), __float_as_uint(dst[lane - 16]), r.epoch);
+        else if (lane < 20)
+            ll_put(yatt + qdim / 4 + qdim / 32 + h * 2 + (lane - 18), (uint32_t)sst[lane - 18], r.epoch);
+    }
+    lds_barrier();
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// S3: attn_output on the attention's Q8, x + proj -> xb (model.rs:1091-1097).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw) {
+    Lds L = Lc;
+    const uint32_t qdim = a.n_head * 64;
+    set_act_k(L, qdim);
+    bool ok = true;
+    const SetRef SO{&Yp->o};
+    const uint32_t t_o = cload(&Yp->t_o), g_o = cload(&Yp->g_o);
+    const uint64_t *yatt = cload(&Yp->att);
+    uint64_t *yxb = cload(&Yp->xb);
+    with_any(t_o, g_o, [&](auto T_, auto G_) {
+        constexpr uint32_t T = decltype(T_)::value;
+        constexpr int G = decltype(G_)::value;
+        Unit<T, G> U[1];
+        TileRef R[1];
+        prefetch_ring<T, G, 1>(SO, gw, nw, U, R);
+        lds_barrier();
+        const uint32_t nwords = qdim / 4 + qdim / 16;
+        ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag,
+                        [&](uint32_t i, uint32_t bits) { L.act.qw[i] = bits; });
+        if (wg_any(!ok, L.vote)) { ok = false; return; }
+        auto out = [&](uint32_t, uint32_t row, float v) {
+            ll_put(yxb + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
+        };
+        gemv_ring<T, G, 1>(SO, L, U, R, gw, nw, out);
+    });
+    if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
+    return ok;
+}
+
+// ---------------------------------------------------------------------------
+// S4: RMSNorm + Q8 of xb, gate/up tile pairs, h = silu(gate) * up
+// (model.rs:1099-1115).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw) {
+    Lds L = Lc;
+    set_act_k(L, a.ne);
+    bool ok = true;
+    const SetRef SGU{&Yp->gu};
+    const uint32_t t_gu = cload(&Yp->t_gu);
+    const float *ffn_norm = cload(&Yp->ffn_norm);
+    const uint64_t *yxb = cload(&Yp->xb);
+    uint64_t *yh = cload(&Yp->h);
+    with_kq(t_gu, [&](auto T_, auto) {
+        constexpr uint32_t T = decltype(T_)::value;
+        constexpr int TPU = QT<T>::TPB;
+        const uint32_t lane = threadIdx.x & 63u;
+        const SetRef &S = SGU;
+        const uint32_t npair = ms_t0(S, 1);
+        const uint32_t p0 = gw;
+        Unit<T, 1> Ug, Uu;
+        TileRef Rg{}, Ru{};
+        if (gw < npair) {
+            Rg = tile_ref(S, p0);
+            Ru = tile_ref(S, npair + p0);
+            Ug.load(Rg.base, Rg.lanes, min(lane, Rg.lanes - 1));
+            Uu.load(Ru.base, Ru.lanes, min(lane, Ru.lanes - 1));
+        }
+        float4 wr[8];
+        load_norm_w(ffn_norm, a.ne, wr);
+        lds_barrier();
+        ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
+        if (wg_any(!ok, L.vote)) { ok = false; return; }
+        trace_detail(a, r, 6);
+        norm_q8(L, a.ne, a.eps, wr, r.neon);
+        trace_detail(a, r, 7);
+        if (gw >= npair) return;
+        Slice<T, 1> SL;
+        SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, lane % ms_upr(S));
+        const uint32_t per_row = ms_upr(S) * TPU;
+        for (uint32_t p = gw; p < npair; p += nw) {
+            if (p != p0) {
+                Rg = tile_ref(S, p);
+                Ru = tile_ref(S, npair + p);
+                Ug.load(Rg.base, Rg.lanes, min(lane, Rg.lanes - 1));
+                Uu.load(Ru.base, Ru.lanes, min(lane, Ru.lanes - 1));
+            }
+            float term[TPU];
+            int isum[TPU];
+            unit_terms<T, 1>(Ug, SL, term, isum);
+            if (lane < Rg.lanes) {
+#pragma unroll
+                for (int t = 0; t < TPU; t++) L.strip[lane * TPU + t] = term[t];
+            }
+            wave_sync();
+            float g = 0.0f;
+            if (lane < Rg.nrows) g = 0.0f + chain_sum(L.strip + lane * per_row, per_row);
+            wave_sync();
+            unit_terms<T, 1>(Uu, SL, term, isum);
+            if (lane < Ru.lanes) {
+#pragma unroll
+                for (int t = 0; t < TPU; t++) L.strip[lane * TPU + t] = term[t];
+            }
+            wave_sync();
+            if (lane < Ru.nrows) {
+                const float u = 0.0f + chain_sum(L.strip + lane * per_row, per_row);
+                const float sg = g / (1.0f + pi_expf(-g));
+                ll_put(yh + Rg.row0 + lane, __float_as_uint(sg * u), r.epoch);
+            }
+            wave_sync();
+        }
+        trace_detail(a, r, 8);
+    });
+    if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
+    return ok;
+}
+
+// ---------------------------------------------------------------------------
+// S5: Q8 of h, ffn_down, xb + proj -> xo (model.rs:1119-1125).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw) {
+    Lds L = Lc;
+    set_act_k(L, a.n_ff);
+    bool ok = true;
+    const SetRef SD{&Yp->down};
+    const uint32_t t_down = cload(&Yp->t_down), g_down = cload(&Yp->g_down);
+    const uint64_t *yh = cload(&Yp->h);
+    uint64_t *yxo = cload(&Yp->xo);
+    with_any(t_down, g_down, [&](auto T_, auto G_) {
+        constexpr uint32_t T = decltype(T_)::value;
+        constexpr int G = decltype(G_)::value;
+        Unit<T, G> U[3];
+        TileRef R[3];
+        prefetch_ring<T, G, 3>(SD, gw, nw, U, R);
+        lds_barrier();
+        ok = wg_poll<23>(yh, a.n_ff, r.epoch, a.abort_flag,
+                         [&](uint32_t i, uint32_t bits) { L.hb[i] = __uint_as_float(bits); });
+        if (wg_any(!ok, L.vote)) { ok = false; return; }
+        trace_detail(a, r, 9);
+        if (threadIdx.x < a.n_ff / 32) {
+            float v[32];
+            const float4 *x4 = reinterpret_cast<const float4 *>(L.hb + 32 * threadIdx.x);
+#pragma unroll
+            for (int j4 = 0; j4 < 8; j4++) {
+                const float4 t = x4[j4];
+                v[4 * j4 + 0] = t.x;
+                v[4 * j4 + 1] = t.y;
+                v[4 * j4 + 2] = t.z;
+                v[4 * j4 + 3] = t.w;
+            }
+            q8_lane(v, L.act.qw + 8 * threadIdx.x, L.act.d + threadIdx.x, L.act.s + threadIdx.x);
+        }
+        lds_barrier();
+        trace_detail(a, r, 10);
+        auto out = [&](uint32_t, uint32_t row, float v) {
+            ll_put(yxo + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
+        };
+        gemv_ring<T, G, 3>(SD, L, U, R, gw, nw, out);
+        trace_detail(a, r, 11);
+    });
+    if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
+    return ok;
+}
+
+__device__ __forceinline__ void amax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Head: output_norm (batch-1 order, model.rs:1136-1143) + Q8 + head GEMV,
+// logits and a (max, first index) pair per workgroup; workgroup 0 reduces
+// the pairs to the greedy id.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, const uint64_t *xin, uint32_t *id_out,
+                           uint32_t gw, uint32_t nw) {
+    Lds L = Lc;
+    set_act_k(L, a.ne);
+    bool ok = true;
+    const SetRef SH{&a.args->head};
+    float best_v = -INFINITY;
+    uint32_t best_i = 0xFFFFFFFFu;
+    with_kq(a.t_head, [&](auto T_, auto) {
+        constexpr uint32_t T = decltype(T_)::value;
+        Unit<T, 1> U[2];
+        TileRef R[2];
+        prefetch_ring<T, 1, 2>(SH, gw, nw, U, R);
+        float4 wr[8];
+        load_norm_w(a.out_norm, a.ne, wr);
+        lds_barrier();
+        if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);
+        if (wg_any(!ok, L.vote)) { ok = false; return; }
+        norm_q8(L, a.ne, a.eps, wr, true);
+        auto out = [&](uint32_t, uint32_t row, float v) {
+            gst(a.logits)[row] = v;
+            amax_merge(best_v, best_i, v, row);
+        };
+        gemv_ring<T, 1, 2>(SH, L, U, R, gw, nw, out);
+    });
+    if (!ok) {
+        if (threadIdx.x == 0) raise_abort(a.abort_flag);
+        return false;
+    }
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int off = 32; off; off >>= 1) {
+        const float ov = __shfl_xor(best_v, off, 64);
+        const uint32_t oi = __shfl_xor(best_i, off, 64);
+        amax_merge(best_v, best_i, ov, oi);
+    }
+    float *sv = L.red + 400;
+    uint32_t *si = reinterpret_cast<uint32_t *>(L.red + 408);
+    if (lane == 0) {
+        sv[wave] = best_v;
+        si[wave] = best_i;
+    }
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < MW; w++) amax_merge(best_v, best_i, sv[w], si[w]);
+        ll_put(a.part + 2 * blockIdx.x, __float_as_uint(best_v), r.epoch);
+        ll_put(a.part + 2 * blockIdx.x + 1, best_i, r.epoch);
+    }
+    if (blockIdx.x != 0) return true;
+    // workgroup 0: reduce every workgroup's pair
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    ok = true;
+    for (uint32_t b = threadIdx.x; b < gridDim.x; b += MT) {
+        uint64_t wv = ll_get(a.part + 2 * b), wi = ll_get(a.part + 2 * b + 1);
+        if (ok) ok = ll_wait(a.part + 2 * b, r.epoch, wv, a.abort_flag);
+        if (ok) ok = ll_wait(a.part + 2 * b + 1, r.epoch, wi, a.abort_flag);
+        amax_merge(bv, bi, __uint_as_float((uint32_t)wv), (uint32_t)wi);
+    }
+    PI_POLL_OR_LEAVE(ok);
+#pragma unroll
+    for (int off = 32; off; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const uint32_t oi = __shfl_xor(bi, off, 64);
+        amax_merge(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    lds_barrier();
+    if (threadIdx.x == 0) {
+        for (uint32_t w = 1; w < MW; w++) amax_merge(bv, bi, sv[w], si[w]);
+        if (bi == 0xFFFFFFFFu) bi = 0;
+        *gst(a.tok_state) = bi;
+        if (id_out) *gst(id_out) = bi;
+    }
+    return true;
+}
+
+// ---------------------------------------------------------------------------
+// The kernel.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__ ap, const uint32_t *tok_src,
+                                                uint32_t *id_out, uint32_t tok_imm, int32_t pos, uint32_t epoch,
+                                                uint32_t flags) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    const Cfg a = load_cfg(ap);
+    Run r{pos, epoch, (flags & 1u) != 0, false};
+    const bool head = (flags & 2u) != 0;
+    const Lds L = carve(smem, a.ne, a.n_ff, a.n_ctx);
+    // wave index in an SGPR: tile indices, tile bases and MatSet fields stay scalar
+    const uint32_t gw = blockIdx.x * MW + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = gridDim.x * MW;
+    trace_mark(a, 0);
+    // embedding of this launch's token (model.rs:857-869) into xt
+    {
+        const uint32_t tok = tok_src ? *gld(tok_src) : tok_imm;
+        const uint8_t *row = a.embd + (uint64_t)tok * a.erow_bytes;
+        unsigned char *rb = reinterpret_cast<unsigned char *>(L.hb);
+        if ((a.erow_bytes & 3u) == 0) {
+            for (uint32_t i = threadIdx.x; i < a.erow_bytes / 4; i += MT)
+                reinterpret_cast<uint32_t *>(rb)[i] = gld(reinterpret_cast<const uint32_t *>(row))[i];
+        } else {
+            for (uint32_t i = threadIdx.x; i < a.erow_bytes; i += MT) rb[i] = gld(row)[i];
+        }
+        lds_barrier();
+        for (uint32_t e = threadIdx.x; e < a.ne; e += MT) xt_set(L, e, embed_elem(rb, a.etype, e));
+        lds_barrier();
+    }
+    trace_mark(a, 1);
+    const uint32_t nb = gridDim.x;
+    for (uint32_t l = 0; l < a.n_layer; l++) {
+        const pi_mega_layer *Y = a.layers + l;
+        r.detail = l == a.n_layer / 2;
+        const uint64_t *xin = l == 0 ? nullptr : cload(&a.layers[l - 1].xo);
+        if (!stage_qkv(a, r, Y, L, xin, gw, nw)) return;
+        trace_mark(a, 2 + 5 * l);
+        for (uint32_t h = nb - 1 - blockIdx.x; h < a.n_head; h += nb)
+            if (!stage_attn(a, r, Y, L, h)) return;
+        trace_mark(a, 3 + 5 * l);
+        if (!stage_o(a, r, Y, L, gw, nw)) return;
+        trace_mark(a, 4 + 5 * l);
+        if (!stage_ffn_up(a, r, Y, L, gw, nw)) return;
+        trace_mark(a, 5 + 5 * l);
+        if (!stage_down(a, r, Y, L, gw, nw)) return;
+        trace_mark(a, 6 + 5 * l);
+    }
+    r.detail = false;
+    if (head) {
+        if (!stage_head(a, r, L, cload(&a.layers[a.n_layer - 1].xo), id_out, gw, nw)) return;
+        trace_mark(a, 2 + 5 * a.n_layer);
+    }
+}
+
+}  // namespace
+
+size_t pi_mega_lds_bytes(uint32_t ne, uint32_t n_ff, uint32_t n_ctx) { return lds_plan(ne, n_ff, n_ctx).total; }
+
+uint32_t pi_mega_blocks(int device, uint32_t ne, uint32_t n_ff, uint32_t n_ctx) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess) return 0;
+    const size_t lds = pi_mega_lds_bytes(ne, n_ff, n_ctx);
+    int occ = 0;
+    auto kern = k_mega;
+    if (hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kern, MT, lds) != hipSuccess || occ < 1) return 0;
+    return (uint32_t)p.multiProcessorCount;
+}
+
+hipError_t pi_launch_mega(const pi_mega_args &a, const pi_mega_args *a_dev, const pi_mega_launch &l, bool neon,
+                          bool head, uint32_t blocks, size_t lds, hipStream_t s) {
+    if (!a_dev || l.epoch == 0 || a.n_layer == 0 || blocks == 0 || a.ne % 32 || a.ne / 32 > MT || a.n_ff / 32 > MT ||
+        a.n_ff % 32 || a.half > 32 || a.n_head == 0 || a.n_kv == 0 || a.n_head % a.n_kv || l.pos < 0 ||
+        (uint32_t)l.pos >= a.n_ctx || lds < pi_mega_lds_bytes(a.ne, a.n_ff, a.n_ctx))
+        return hipErrorInvalidValue;
+    const void *kern = (const void *)k_mega;
+    hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    const pi_mega_args *ap = a_dev;
+    const uint32_t *tok_src = l.tok_src;
+    uint32_t *id_out = l.id_out;
+    uint32_t tok_imm = l.tok_imm;
+    int32_t pos = l.pos;
+    uint32_t epoch = l.epoch;
+    uint32_t flags = (neon ? 1u : 0u) | (head ? 2u : 0u);
+    void *args[] = {&ap, &tok_src, &id_out, &tok_imm, &pos, &epoch, &flags};
+    return hipLaunchCooperativeKernel(kern, dim3(blocks), dim3(MT), args, (unsigned)lds, s);
+}

@@ -16,6 +16,15 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden" / "minicpm2b_greedy.json"
 
 
+@pytest.fixture(params=["persistent", "per_stage"], autouse=True)
+def engine_mode(request, backend):
+    """Every engine test runs on the persistent kernel (one cooperative
+    launch per token) and on the per-stage kernels."""
+    backend.use_persistent(request.param == "persistent")
+    yield request.param
+    backend.use_persistent(True)
+
+
 @pytest.fixture(scope="module")
 def tiny(pih):
     return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000), seed=7)
@@ -30,10 +39,11 @@ def _bits_equal(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
 
-def test_tiny_forward_logits(pih, backend, oracle, tiny):
+def test_tiny_forward_logits(pih, backend, oracle, tiny, engine_mode):
     """Batch-1 forwards: logits within the contract's tolerance, and in fact
     bit-identical since every float op keeps the reference order."""
     eng = pih.HipEngine(backend, tiny, n_ctx=128)
+    assert backend.persistent_active() == (engine_mode == "persistent")
     ref = oracle.OracleEngine(tiny, n_ctx=128, threads=4)
     ids = [5, 17, 999, 0, 123, 456, 7, 8] + [(i * 131 + 3) % 1000 for i in range(70)]
     for pos, tok in enumerate(ids):
@@ -123,7 +133,7 @@ def test_tiny_context_full_and_eog(pih, backend, oracle, tiny):
         eng.forward([1], [50])
 
 
-def test_minicpm2b_first_64_greedy_ids(pih, backend):
+def test_minicpm2b_first_64_greedy_ids(pih, backend, engine_mode):
     """Full-size synthetic model; ids from the committed oracle fixture."""
     g = json.loads(GOLDEN.read_text())
     spec = pih.minicpm2b_spec()
@@ -132,5 +142,6 @@ def test_minicpm2b_first_64_greedy_ids(pih, backend):
     for name, h in g["tensor_sha256"].items():
         assert hashlib.sha256(model.tensors[name][3].tobytes()).hexdigest() == h, name
     eng = pih.HipEngine(backend, model, n_ctx=len(g["prompt"]) + g["n_gen"] + 8)
+    assert backend.persistent_active() == (engine_mode == "persistent")
     ids, st = eng.generate(g["prompt"], g["n_gen"])
     assert ids == g["gen_ids"], f"first mismatch at {next(i for i, (a, b) in enumerate(zip(ids, g['gen_ids'])) if a != b)}"
