@@ -19,6 +19,7 @@
 #include "pi_decode.h"
 #include "pi_kernels.h"
 #include "pi_mega.h"
+#include "pi_prefill.h"
 
 struct pi_tensor {
     pi_layout L;
@@ -75,6 +76,13 @@ struct Engine {
     uint64_t *mega_trace = nullptr;  // per-workgroup stage timestamps when tracing
     uint32_t mega_blocks = 0, epoch = 0;
     size_t mega_lds = 0;
+    // batched prefill (pi_prefill.hip): token-major chunk buffers
+    bool pf_ok = false;
+    float *pfX = nullptr, *pfQ = nullptr, *pfK = nullptr, *pfV = nullptr, *pfG = nullptr, *pfU = nullptr;
+    int8_t *pfq = nullptr;
+    float *pfd = nullptr;
+    int32_t *pfs = nullptr;
+    uint32_t *pf_ids = nullptr;
 };
 
 }  // namespace
@@ -86,6 +94,7 @@ struct pi_ctx {
     bool fail_next = false;
     bool use_graphs = true;   // replay captured graphs (else launch each kernel)
     bool use_persistent = true;  // one persistent kernel per token when the model fits
+    bool use_batch_prefill = true;  // chunks of 2..32 tokens on the MFMA prefill kernels
     std::atomic<int> stop{0};
     std::map<std::pair<uintptr_t, size_t>, pi_tensor *> wcache;
     // grow-only IO buffers of matvec / test hooks (opencl.rs:461-482)
@@ -253,6 +262,9 @@ void engine_free(Engine *e) {
     free_tensor(e->head);
     for (void *p : {(void *)e->mega_dev, (void *)e->mega_layers, (void *)e->mega_words, (void *)e->mega_part,
                     (void *)e->mega_abort, (void *)e->mega_trace})
+        dfree(p);
+    for (void *p : {(void *)e->pfX, (void *)e->pfQ, (void *)e->pfK, (void *)e->pfV, (void *)e->pfG, (void *)e->pfU,
+                    (void *)e->pfq, (void *)e->pfd, (void *)e->pfs, (void *)e->pf_ids})
         dfree(p);
     for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
                     (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->h,
@@ -516,6 +528,62 @@ int build_mega(pi_ctx *c, Engine &e) {
 
 bool use_mega(const pi_ctx *c, const Engine &e) { return c->use_persistent && e.mega_ok; }
 
+// Buffers of the batched prefill; leaves pf_ok false (tokens are evaluated
+// one by one) when the model is outside the kernels' limits.
+int build_prefill(pi_ctx *c, Engine &e) {
+    e.pf_ok = false;
+    const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
+    if (e.dh != 64 || e.n_embd / 32 > 256 || e.n_rot / 2 > 32) return PI_OK;
+    int maxlds = 0;
+    if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;
+    if (pi_pf_attn_lds_bytes(e.n_ctx) > (size_t)maxlds) return PI_OK;
+    const uint64_t T = PI_PF_MAX_TOK;
+    const uint64_t kmax = std::max(std::max(e.n_embd, e.n_ff), qdim);
+    int r;
+    if ((r = dalloc(c, &e.pfX, T * e.n_embd)) || (r = dalloc(c, &e.pfQ, T * qdim)) || (r = dalloc(c, &e.pfK, T * kdim)) ||
+        (r = dalloc(c, &e.pfV, T * kdim)) || (r = dalloc(c, &e.pfG, T * e.n_ff)) || (r = dalloc(c, &e.pfU, T * e.n_ff)) ||
+        (r = dalloc(c, &e.pfq, T * kmax)) || (r = dalloc(c, &e.pfd, T * kmax / 32)) || (r = dalloc(c, &e.pfs, T * kmax / 32)) ||
+        (r = dalloc(c, &e.pf_ids, 2 * T)))
+        return r;
+    e.pf_ok = true;
+    return PI_OK;
+}
+
+bool use_pf(const pi_ctx *c, const Engine &e) { return c->use_batch_prefill && e.pf_ok; }
+
+pi_pf_mat pfmat(const pi_tensor *t) { return pi_pf_mat{t->dev, t->L}; }
+
+// One chunk of ntok (2..32) tokens at positions pos0.. through every layer
+// on the batched prefill kernels; the residual stream ends in pfX.
+hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, uint32_t pos0, uint32_t ntok) {
+    hipStream_t s = c->stream;
+    hipError_t r;
+#define K(expr) do { if ((r = (expr)) != hipSuccess) return r; } while (0)
+    const float scale = 1.0f / sqrtf((float)e.dh);
+    const pi_pf_q8 A{e.pfq, e.pfd, e.pfs};
+    K(pi_pf_embed(e.embd, e.embd_type, e.embd_row_bytes, ids_dev, ntok, e.n_embd, e.pfX, s));
+    for (uint32_t l = 0; l < e.n_layer; l++) {
+        const Layer &L = e.layers[l];
+        float *kc = e.kc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        float *vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
+        K(pi_pf_norm_q8(e.pfX, L.attn_norm, e.n_embd, e.eps, ntok, A, s));
+        K(pi_pf_gemm(pfmat(L.q), A, ntok, e.pfQ, false, s));
+        K(pi_pf_gemm(pfmat(L.k), A, ntok, e.pfK, false, s));
+        K(pi_pf_gemm(pfmat(L.v), A, ntok, e.pfV, false, s));
+        K(pi_pf_rope_kv(e.pfQ, e.pfK, e.pfV, e.cos_tab, e.sin_tab, pos0, ntok, e.n_head, e.n_kv, e.n_rot / 2, kc, vc,
+                        e.n_ctx, s));
+        K(pi_pf_attn(e.pfQ, kc, vc, pos0, ntok, e.n_head, e.n_kv, e.n_ctx, scale, A, s));
+        K(pi_pf_gemm(pfmat(L.o), A, ntok, e.pfX, true, s));
+        K(pi_pf_norm_q8(e.pfX, L.ffn_norm, e.n_embd, e.eps, ntok, A, s));
+        K(pi_pf_gemm(pfmat(L.gate), A, ntok, e.pfG, false, s));
+        K(pi_pf_gemm(pfmat(L.up), A, ntok, e.pfU, false, s));
+        K(pi_pf_swiglu_q8(e.pfG, e.pfU, ntok, e.n_ff, A, s));
+        K(pi_pf_gemm(pfmat(L.down), A, ntok, e.pfX, true, s));
+    }
+    return hipSuccess;
+#undef K
+}
+
 // One token through the persistent kernel (layers, and the head when `head`).
 hipError_t mega_token(const pi_ctx *c, Engine &e, int32_t pos, uint32_t tok_imm, const uint32_t *tok_src,
                       uint32_t *id_out, bool neon, bool head) {
@@ -663,6 +731,12 @@ int pi_hip_use_graphs(pi_ctx *c, int enable) {
 int pi_hip_use_persistent(pi_ctx *c, int enable) {
     if (!c) return PI_E_INVALID;
     c->use_persistent = enable != 0;
+    return PI_OK;
+}
+
+int pi_hip_use_batch_prefill(pi_ctx *c, int enable) {
+    if (!c) return PI_E_INVALID;
+    c->use_batch_prefill = enable != 0;
     return PI_OK;
 }
 
@@ -1025,6 +1099,7 @@ int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
     if (hipMemset(e->logits, 0, vocab * 4) != hipSuccess) { engine_free(e); return fail(c, PI_E_HIP, "memset"); }
     TRY(build_graphs(c, *e));
     TRY(build_mega(c, *e));
+    TRY(build_prefill(c, *e));
 #undef TRY
     c->eng = e;
     return PI_OK;
@@ -1037,6 +1112,32 @@ static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int 
         if (pos[i] < 0 || (uint32_t)pos[i] >= e->n_ctx) return fail(c, PI_E_CONTEXT_FULL, "context full");
         if (ids[i] >= e->n_vocab) return fail(c, PI_E_INVALID, "token %u out of vocab", ids[i]);
         if (i > 0 && pos[i] <= pos[i - 1]) return fail(c, PI_E_INVALID, "batch positions must increase");
+    }
+    bool consecutive = true;
+    for (int i = 1; i < b; i++) consecutive &= pos[i] == pos[0] + i;
+    if (b > 1 && consecutive && use_pf(c, *e)) {
+        // a batch of more than one token: every token in the multi-token
+        // orders, in chunks of at most 32 on the batched prefill kernels
+        if (want_logits) {
+            int r = set_state(c, *e, pos[b - 1], ids[b - 1], 0, 0);
+            if (r) return r;
+        }
+        uint32_t last_nt = 0;
+        for (int off = 0; off < b; off += (int)PI_PF_MAX_TOK) {
+            if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
+            const uint32_t nt = std::min<uint32_t>(PI_PF_MAX_TOK, (uint32_t)(b - off));
+            HIPC(c, hipMemcpyAsync(e->pf_ids, ids + off, nt * 4, hipMemcpyHostToDevice, c->stream));
+            HIPC(c, pf_chunk(c, *e, e->pf_ids, (uint32_t)pos[off], nt));
+            last_nt = nt;
+        }
+        if (want_logits) {
+            HIPC(c, hipMemcpyAsync(e->x, e->pfX + (uint64_t)(last_nt - 1) * e->n_embd, (size_t)e->n_embd * 4,
+                                   hipMemcpyDeviceToDevice, c->stream));
+            HIPC(c, enqueue_logits(*e, c->stream));
+            HIPC(c, enqueue_step(*e, PI_STEP_ARGMAX, nullptr, c->stream));
+        }
+        HIPC(c, hipStreamSynchronize(c->stream));
+        return PI_OK;
     }
     if (use_mega(c, *e)) {
         for (int i = 0; i < b; i++) {
@@ -1137,6 +1238,47 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     // a chunk of more than one token take the scalar-order graph; the last
     // prompt token also computes logits and the first greedy id.
     const size_t last_chunk = (n - reused) % chunk == 0 ? chunk : (n - reused) % chunk;
+    if (use_pf(c, *e)) {
+        // Reference chunks of 32 from `reused`: a chunk of more than one token
+        // runs on the batched prefill kernels; a chunk of one (only the last
+        // can be) in the batch-1 order.  The last chunk also computes the
+        // logits and the first greedy id of its last token.
+        while (off < n) {
+            if (c->stop.load()) { stopped = true; break; }
+            const size_t end = std::min(n, off + chunk);
+            const bool last = end == n;
+            if (end - off == 1) {
+                if (mega) {
+                    HIPC(c, mega_token(c, *e, (int32_t)off, prompt[off], nullptr, e->ids, true, true));
+                } else {
+                    if ((r = set_state(c, *e, (int32_t)off, prompt[off], 0, (uint32_t)off))) return r;
+                    HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
+                    HIPC(c, run_step(c, *e, STEP_DECODE));
+                }
+            } else {
+                if (last && (r = set_state(c, *e, (int32_t)(n - 1), prompt[n - 1], 0, (uint32_t)(n - 1)))) return r;
+                HIPC(c, pf_chunk(c, *e, e->prompt + off, (uint32_t)off, (uint32_t)(end - off)));
+                if (last) {
+                    HIPC(c, hipMemcpyAsync(e->x, e->pfX + (uint64_t)(end - off - 1) * e->n_embd,
+                                           (size_t)e->n_embd * 4, hipMemcpyDeviceToDevice, c->stream));
+                    HIPC(c, enqueue_logits(*e, c->stream));
+                    HIPC(c, enqueue_step(*e, PI_STEP_ARGMAX, e->ids, c->stream));
+                }
+            }
+            HIPC(c, hipStreamSynchronize(c->stream));
+            if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); return r; }
+            e->kv_tokens.insert(e->kv_tokens.end(), prompt + off, prompt + end);
+            off = end;
+        }
+        if (stopped) {
+            snprintf(st->stop, sizeof st->stop, "user_stop");
+            st->prefill_tokens = (uint32_t)(off - reused);
+            e->kv_tokens.clear();
+            st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+            return PI_OK;
+        }
+        goto prefill_done;
+    }
     while (off + 1 < n) {
         if (c->stop.load()) { stopped = true; break; }
         size_t end = std::min(n - 1, off + chunk);
@@ -1162,6 +1304,7 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     HIPC(c, hipStreamSynchronize(c->stream));
     if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); return r; }
     e->kv_tokens.push_back(prompt[n - 1]);
+prefill_done:
     off = n;
     st->prefill_tokens = (uint32_t)(off - reused);
     st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();

@@ -1,0 +1,49 @@
+// Launchers of the batched prefill kernels (pi_prefill.hip): one chunk of up
+// to 32 prompt tokens evaluated together, in the float orders the reference
+// uses for a batch of more than one token (model.rs:812-822, 1028-1038).
+// All launch on `s` and return hipSuccess or the launch error.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include "pi_common.h"
+
+constexpr uint32_t PI_PF_MAX_TOK = 32;
+
+// A weight matrix in the tiled layout (pi_common.h), as the prefill GEMM reads it.
+struct pi_pf_mat {
+    const uint8_t *w;
+    pi_layout L;
+};
+
+// Token-major activations of a chunk: row t of a [ntok][n] matrix at t * n.
+// Q8 activations use the Q8Act lane-major layout (quant_int.rs:46-53):
+// q[t * k + j], d[t * k/32 + blk], sum[t * k/32 + blk].
+struct pi_pf_q8 {
+    int8_t *q;
+    float *d;
+    int32_t *s;
+};
+
+// X[t] = token_embd row ids[t] (dequant_row, model.rs:857-869).
+hipError_t pi_pf_embed(const uint8_t *embd, uint32_t etype, uint64_t row_bytes, const uint32_t *ids_dev, uint32_t ntok,
+                       uint32_t ne, float *X, hipStream_t s);
+// RMSNorm of every token in the scalar order (model.rs:812-822), then Q8.
+hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps, uint32_t ntok, pi_pf_q8 out,
+                         hipStream_t s);
+// out[t][row] = W a_t (resid: out[t][row] += W a_t); int8 MFMA for the integer
+// sums of every 32- (Q6_K: 16-) element group, the reference's float
+// epilogue in block order per (row, token).
+hipError_t pi_pf_gemm(const pi_pf_mat &W, pi_pf_q8 act, uint32_t ntok, float *out, bool resid, hipStream_t s);
+// RoPE of Q and K of every token (model.rs:953-979) and the K/V rows of
+// positions pos0..pos0+ntok-1 written into this layer's caches (984-992).
+hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *cos_tab, const float *sin_tab,
+                         uint32_t pos0, uint32_t ntok, uint32_t n_head, uint32_t n_kv, uint32_t half, float *kc,
+                         float *vc, uint32_t n_ctx, hipStream_t s);
+// Attention of every token over positions 0..its own (model.rs:993-1087,
+// multi-token orders), then Q8 of the output.
+hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
+                      uint32_t n_kv, uint32_t n_ctx, float scale, pi_pf_q8 out, hipStream_t s);
+size_t pi_pf_attn_lds_bytes(uint32_t n_ctx);
+// h = silu(gate) * up (model.rs:1111-1115), then Q8 of h.
+hipError_t pi_pf_swiglu_q8(const float *G, const float *U, uint32_t ntok, uint32_t n_ff, pi_pf_q8 out, hipStream_t s);

@@ -45,7 +45,7 @@ EXPORTS = [
     "pi_hip_model_bind", "pi_hip_forward", "pi_hip_logits", "pi_hip_argmax", "pi_hip_generate",
     "pi_hip_kv_write", "pi_hip_kv_read", "pi_hip_kv_fill_normal", "pi_hip_kv_set_tokens",
     "pi_hip_request_stop", "pi_hip_clear_stop", "pi_hip_use_graphs", "pi_hip_last_decode_us",
-    "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
+    "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
     "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor",
     "pi_quantize_row",
 ]
@@ -138,6 +138,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_hip_use_graphs": (i32, [vp, i32]),
         "pi_hip_use_persistent": (i32, [vp, i32]),
         "pi_hip_persistent_active": (i32, [vp]),
+        "pi_hip_use_batch_prefill": (i32, [vp, i32]),
         "pi_hip_stage_trace": (i32, [vp, i32]),
         "pi_hip_stage_trace_read": (i32, [vp, vp, C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
         "pi_hip_last_decode_us": (i32, [vp, C.POINTER(C.c_double)]),
@@ -341,6 +342,10 @@ class HipBackend:
     def use_persistent(self, enable: bool) -> None:
         """Engine tokens on the persistent kernel (default) or per-stage kernels."""
         self.check(self.lib.pi_hip_use_persistent(self.ctx, int(enable)))
+
+    def use_batch_prefill(self, enable: bool) -> None:
+        """Prompt chunks on the batched MFMA prefill kernels (default) or token by token."""
+        self.check(self.lib.pi_hip_use_batch_prefill(self.ctx, int(enable)))
 
     def persistent_active(self) -> bool:
         return self.lib.pi_hip_persistent_active(self.ctx) == 1

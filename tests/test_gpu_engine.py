@@ -16,13 +16,17 @@ pytestmark = pytest.mark.gpu
 GOLDEN = Path(__file__).parent / "golden" / "minicpm2b_greedy.json"
 
 
-@pytest.fixture(params=["persistent", "per_stage"], autouse=True)
+@pytest.fixture(params=["persistent", "per_stage", "token_prefill"], autouse=True)
 def engine_mode(request, backend):
     """Every engine test runs on the persistent kernel (one cooperative
-    launch per token) and on the per-stage kernels."""
-    backend.use_persistent(request.param == "persistent")
-    yield request.param
+    launch per token) and on the per-stage kernels, with multi-token chunks
+    on the batched MFMA prefill kernels; and once more with every prompt
+    token evaluated on its own."""
+    backend.use_persistent(request.param != "per_stage")
+    backend.use_batch_prefill(request.param != "token_prefill")
+    yield "per_stage" if request.param == "per_stage" else "persistent"
     backend.use_persistent(True)
+    backend.use_batch_prefill(True)
 
 
 @pytest.fixture(scope="module")
