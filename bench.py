@@ -19,7 +19,15 @@ Also measured here:
   cpu_baseline -- the CPU oracle's decode tok/s on a bounded sample (32-id
                prompt, 9 greedy tokens) with every host thread.
 
+  prefill  -- the 2048-token prompt of the same model on the batched int8-MFMA
+               prefill kernels (64 chunks of 32), then the prompt extended by
+               512 tokens reusing the 2048 cached positions;
+  long_context -- decode at 4096 and 16384 positions of N(0,1) KV
+               (737 280 KV bytes per position on top of the weights).
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+       python bench.py --profile-gemv   (GEMV launches and a 256 MiB device
+                                         copy only, for counter runs)
 """
 import argparse
 import json
@@ -41,6 +49,10 @@ Q4K_LAUNCH_BYTES = Q4K_ROWS * (Q4K_K // 256) * 144 + Q4K_K * 4 + Q4K_ROWS * 4   
 Q6K_ROWS, Q6K_K = 122753, 2304
 Q6K_LAUNCH_BYTES = Q6K_ROWS * (Q6K_K // 256) * 210 + Q6K_K * 4 + Q6K_ROWS * 4     # 232 503 398
 MODEL_SEED, PROMPT_SEED, N_PROMPT = 1234, 77, 128
+# HBM bytes per Q4_K GEMV launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each
+# scaled by what the counter reads for a 256 MiB copy (read x1.9997, write x1.0):
+# profiles/gemv_q4k_5760x2304_traffic.md
+Q4K_TRAFFIC_BYTES = round((3751.1 * 1.9997 + 45.0 * 1.0) * 1024)
 
 
 def splitmix_ids(seed: int, n: int, vocab: int) -> list:
@@ -73,6 +85,47 @@ def time_gemv(b, t, rows, k, gen, copies, iters):
     return us
 
 
+def bench_prefill(b, model, spec):
+    """2048-token prompt, then +512 tokens with prefix reuse (model.rs:1258-1268)."""
+    ids = splitmix_ids(91, 2048 + 512, spec.n_vocab)
+    eng = pih.HipEngine(b, model, n_ctx=2048 + 512 + 16)
+    eng.generate(ids[:96], 1)                       # first launches of every prefill kernel
+    eng.forward([ids[0]], [0], want_logits=False)   # a manual forward drops the reusable prefix
+    _, sa = eng.generate(ids[:2048], 1)
+    _, sb = eng.generate(ids, 1)
+    return {"prompt_tokens": 2048, "prefill_ms": round(sa["prefill_ms"], 2),
+            "tok_s": round(2048 / (sa["prefill_ms"] / 1000.0), 1), "chunk_tokens": 32,
+            "extension": {"new_tokens": sb["prefill_tokens"], "reused_tokens": sb["prefill_cached_tokens"],
+                          "prefill_ms": round(sb["prefill_ms"], 2),
+                          "tok_s": round(sb["prefill_tokens"] / (sb["prefill_ms"] / 1000.0), 1)}}
+
+
+def bench_long_context(b, model, n_fill, steps, wbytes):
+    """Decode after N(0,1) K/V for positions 0..n_fill-1 (seed 4242)."""
+    eng = pih.HipEngine(b, model, n_ctx=n_fill + steps + 16)
+    eng.kv_fill_normal(n_fill, 4242)
+    eng.kv_set_tokens([0] * n_fill)
+    _, st = eng.generate([0] * n_fill + [17], steps + 1)   # reuses n_fill, evaluates token 17, then decodes
+    tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
+    kv_bytes = 737280 * (n_fill + steps // 2)
+    per_tok = wbytes + kv_bytes
+    return {"context": n_fill, "tok_s": round(tps, 2), "gen_tokens": st["gen_tokens"],
+            "device_us_per_forward": round(eng.last_decode_us(), 1), "reused": st["prefill_cached_tokens"],
+            "bytes_per_token": per_tok, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
+            "frac": round(tps * per_tok / (HBM_PEAK_GBS * 1e9), 4)}
+
+
+def profile_gemv(b):
+    """Q4_K GEMV launches over 70 weight copies and one 256 MiB device copy:
+    a short program for rocprofv3 counter runs (FETCH_SIZE / WRITE_SIZE)."""
+    us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 210)
+    n = 256 << 20
+    src, dst = b.alloc(n), b.alloc(n)
+    b.copy_d2d(dst, src, n)
+    b.synchronize()
+    print(json.dumps({"profile": "gemv", "q4k_us_per_launch": round(us, 3), "copy_bytes": n}), flush=True)
+
+
 def cpu_baseline(model, prompt):
     from oracle import oracle
     threads = min(os.cpu_count() or 1, 16)
@@ -92,6 +145,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graphs", action="store_true", help="launch kernels one by one (for profilers)")
+    ap.add_argument("--no-extra", action="store_true", help="skip the prefill and long-context sections")
+    ap.add_argument("--profile-gemv", action="store_true", help="GEMV launches and a device copy only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one MI355X only: multi-GPU runs are not part of this build "
@@ -101,6 +156,9 @@ def main():
     b = pih.HipBackend(0)
     b.use_graphs(not args.no_graphs)
     log(f"device: {b.name()}")
+    if args.profile_gemv:
+        profile_gemv(b)
+        return
 
     # -- roofline: dominant kernel, config-1 shape, HBM-cold -----------------
     q4k_us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
@@ -136,6 +194,13 @@ def main():
         if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED:
             match = ids[: g["n_gen"]] == g["gen_ids"]
 
+    prefill = long_ctx = None
+    if not args.no_extra:
+        prefill = bench_prefill(b, model, spec)
+        log(f"prefill: {prefill}")
+        long_ctx = [bench_long_context(b, model, n, 16, wbytes) for n in (4096, 16384)]
+        log(f"long context: {long_ctx}")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(model, prompt)
@@ -158,7 +223,7 @@ def main():
                                "hidden 2304, 36x64 MHA, FFN 5760, vocab 122753, f32 KV",
                    "prompt_tokens": N_PROMPT, "gen_tokens": st["gen_tokens"], "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(q4k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(q4k_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(q4k_gbs / HBM_PEAK_GBS, 4), "traffic": Q4K_TRAFFIC_BYTES,
                      "kernel": "Q4_K GEMV 5760x2304 (k_gemv<12,1,0,1>)", "us_per_launch": round(q4k_us, 3),
                      "bytes_per_launch": Q4K_LAUNCH_BYTES},
         "q6k_head_gemv": {"achieved": round(q6k_gbs, 1), "unit": "GB/s", "frac": round(q6k_gbs / HBM_PEAK_GBS, 4),
@@ -168,6 +233,8 @@ def main():
                                    "frac": round(tps * wbytes / (HBM_PEAK_GBS * 1e9), 4),
                                    "device_us_per_forward": round(dev_us, 2)},
         "greedy_first_64_match_oracle": match,
+        "prefill": prefill,
+        "long_context": long_ctx,
         "cpu_baseline": cpu,
         "wall_s": round(time.time() - t_start, 1),
     }

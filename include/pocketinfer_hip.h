@@ -115,6 +115,10 @@ int  pi_hip_dev_alloc(pi_ctx *ctx, size_t bytes, void **out);
 void pi_hip_dev_free(pi_ctx *ctx, void *p);
 int  pi_hip_copy_h2d(pi_ctx *ctx, void *dst_dev, const void *src, size_t bytes);
 int  pi_hip_copy_d2h(pi_ctx *ctx, void *dst, const void *src_dev, size_t bytes);
+/* Device-to-device copy on the context stream (asynchronous): a streaming
+ * copy kernel for the 16-byte-aligned bulk, so HBM counters can be calibrated
+ * against a copy of known size. */
+int  pi_hip_copy_d2d(pi_ctx *ctx, void *dst_dev, const void *src_dev, size_t bytes);
 
 /* Stream control.  pi_hip_set_stream makes the context launch on a caller
  * stream (a hipStream_t passed as a plain pointer; NULL restores its own). */
@@ -198,7 +202,8 @@ int  pi_hip_kv_write(pi_ctx *ctx, uint32_t layer, uint32_t kv_head, uint32_t pos
 int  pi_hip_kv_read(pi_ctx *ctx, uint32_t layer, uint32_t kv_head, uint32_t pos0, uint32_t n,
                     float *k, float *v);
 /* Fills the KV rows of positions [0, n) of every layer and head with
- * N(0,1) draws of a seeded generator, on the device (long-context setup). */
+ * N(0,1) draws of a seeded generator, on the device (long-context setup);
+ * pi_synth_kv_normal gives the same values on the host. */
 int  pi_hip_kv_fill_normal(pi_ctx *ctx, uint32_t n, uint64_t seed);
 /* Marks positions [0, n) of the KV cache as holding these tokens, so that
  * forward/generate may continue from them (used after pi_hip_kv_write). */
@@ -242,6 +247,10 @@ int pi_synth_q4k_random(uint64_t seed, size_t rows, size_t k, float dlo, float d
 /* Random Q6_K blocks: ql/qh uniform bytes; scales uniform in [-64, 63];
  * d ~ U[dlo, dhi] as f16. */
 int pi_synth_q6k_random(uint64_t seed, size_t rows, size_t k, float dlo, float dhi, uint8_t *out);
+/* The values pi_hip_kv_fill_normal writes for positions p0..p0+n-1 of
+ * layer-major kv head lh (= layer * n_kv + head): k and v get n * dh floats,
+ * [position][dim].  Host-only, bit-identical to the device fill. */
+int pi_synth_kv_normal(uint64_t seed, uint32_t lh, uint32_t p0, uint32_t n, uint32_t dh, float *k, float *v);
 /* n draws of N(mean, std) (Marsaglia polar method). */
 int pi_synth_normal(uint64_t seed, size_t n, float mean, float std, float *out);
 /* rows x k weights ~ N(mean, std), quantized row by row to ggml_type (F32

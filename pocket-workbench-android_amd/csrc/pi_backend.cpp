@@ -835,6 +835,19 @@ int pi_hip_copy_h2d(pi_ctx *c, void *dst, const void *src, size_t bytes) {
     return PI_OK;
 }
 
+int pi_hip_copy_d2d(pi_ctx *c, void *dst, const void *src, size_t bytes) {
+    if (!c || !dst || !src) return PI_E_INVALID;
+    size_t bulk = 0;
+    if ((((uintptr_t)dst | (uintptr_t)src) & 15) == 0) {
+        bulk = bytes & ~(size_t)15;
+        HIPC(c, pi_launch_copy16(src, dst, bulk / 16, c->stream));
+    }
+    if (bytes > bulk)
+        HIPC(c, hipMemcpyAsync((uint8_t *)dst + bulk, (const uint8_t *)src + bulk, bytes - bulk,
+                               hipMemcpyDeviceToDevice, c->stream));
+    return PI_OK;
+}
+
 int pi_hip_copy_d2h(pi_ctx *c, void *dst, const void *src, size_t bytes) {
     if (!c || !dst || !src) return PI_E_INVALID;
     HIPC(c, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, c->stream));

@@ -54,11 +54,11 @@ PI_DM float pi_expf(float x) {
     return (float)pi_exp_d((double)x);
 }
 
-// log(x) for finite x > 0 (host use: the RoPE base).
-inline double pi_log_d(double x) {
+// log(x) for finite x > 0.
+PI_DM double pi_log_d(double x) {
     const double LN2_HI = 6.93147180369123816490e-01, LN2_LO = 1.90821492927058770002e-10;
     int e = 0;
-    double m = std::frexp(x, &e);
+    double m = frexp(x, &e);
     if (m < 0.70710678118654752440) { m = m * 2.0; e = e - 1; }
     double t = (m - 1.0) / (m + 1.0), t2 = t * t;
     double s = 1.0 / 31.0;
@@ -68,7 +68,7 @@ inline double pi_log_d(double x) {
 }
 
 // sin and cos for |x| < 2^20.
-inline void pi_sincos_d(double x, double *s, double *c) {
+PI_DM void pi_sincos_d(double x, double *s, double *c) {
     const double TWO_OVER_PI = 6.36619772367581382433e-01;
     const double PIO2_1 = 1.57079632673412561417e+00;
     const double PIO2_2 = 6.07710050630396597660e-11;
@@ -111,6 +111,29 @@ inline void pi_sincos_d(double x, double *s, double *c) {
     case 2: *s = -sr; *c = -cr; break;
     default: *s = -cr; *c = sr; break;
     }
+}
+
+// Seeded N(0,1) pair for element (layer*n_kv + head, position, dim) of the
+// K and V caches (long-context setup): SplitMix64 finalizer hashing of the
+// key, Box-Muller in IEEE double with the functions above, so the host and
+// the device produce the same bits.  Independent of how many positions are
+// filled.
+PI_DM uint64_t pi_mix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+PI_DM void pi_kv_normal(uint64_t seed, uint32_t lh, uint32_t p, uint32_t d, float *k, float *v) {
+    const uint64_t key = ((uint64_t)lh << 32) | ((uint64_t)p << 8) | (uint64_t)d;
+    const uint64_t z1 = pi_mix64(seed ^ pi_mix64(key)), z2 = pi_mix64(z1);
+    const double u1 = ((double)(z1 >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(z2 >> 11) * (1.0 / 9007199254740992.0);
+    const double rad = pi_exp_d(0.5 * pi_log_d(-2.0 * pi_log_d(u1)));   // sqrt(-2 ln u1)
+    double sn, cs;
+    pi_sincos_d(6.28318530717958647692 * u2, &sn, &cs);
+    *k = (float)(rad * cs);
+    *v = (float)(rad * sn);
 }
 
 inline float pi_cosf(float x) { double s, c; pi_sincos_d((double)x, &s, &c); return (float)c; }

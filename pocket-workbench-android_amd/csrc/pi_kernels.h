@@ -25,6 +25,8 @@ hipError_t pi_launch_q8(const float *x, uint32_t k, uint32_t b, int8_t *q, float
                         hipStream_t s);
 
 // Fills n positions of every (layer, kv head) with N(0,1) draws.
+// dst = src for `words` 16-byte words (both 16-byte aligned).
+hipError_t pi_launch_copy16(const void *src, void *dst, uint64_t words, hipStream_t s);
 hipError_t pi_launch_kv_fill(float *kc, float *vc, uint32_t n_layer_heads, uint32_t n_ctx,
                              uint32_t dh, uint32_t n, uint64_t seed, hipStream_t s);
 

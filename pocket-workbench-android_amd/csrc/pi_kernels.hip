@@ -50,28 +50,34 @@ __global__ void k_q8(const float *__restrict__ x, uint32_t k, uint32_t b, int8_t
     q8_block32(v, (int)j, q + (uint64_t)bi * k + blk * 32, d + (uint64_t)bi * nb + blk, sum + (uint64_t)bi * nb + blk, ok);
 }
 
-// N(0,1) fill: counter-based SplitMix64 and Box-Muller.
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-    z += 0x9E3779B97F4A7C15ull;
-    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
-    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
-    return z ^ (z >> 31);
-}
+// N(0,1) fill of positions [0, n) of every (layer, kv head): pi_kv_normal.
 __global__ void k_kv_fill(float *kc, float *vc, uint32_t nlh, uint32_t n_ctx, uint32_t dh, uint32_t n, uint64_t seed) {
     const uint64_t per = (uint64_t)n * dh, total = (uint64_t)nlh * per;
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
-        uint64_t lh = i / per, r = i % per;
-        uint64_t dst = lh * (uint64_t)n_ctx * dh + r;
-        uint64_t z = mix64(seed ^ mix64(i));
-        float u1 = ((float)(z >> 40) + 0.5f) * (1.0f / 16777216.0f);
-        float u2 = (float)((z >> 16) & 0xFFFFFFu) * (1.0f / 16777216.0f);
-        float rad = sqrtf(-2.0f * logf(u1));
-        kc[dst] = rad * cospif(2.0f * u2);
-        vc[dst] = rad * sinpif(2.0f * u2);
+        const uint32_t lh = (uint32_t)(i / per), r = (uint32_t)(i % per);
+        const uint32_t p = r / dh, d = r % dh;
+        float k, v;
+        pi_kv_normal(seed, lh, p, d, &k, &v);
+        const uint64_t dst = (uint64_t)lh * n_ctx * dh + r;
+        kc[dst] = k;
+        vc[dst] = v;
     }
 }
 
+// dst[i] = src[i] for n 16-byte words: a plain streaming copy (one read and
+// one write of each byte) whose counter readings calibrate HBM traffic.
+__global__ void k_copy16(const uint4 *__restrict__ src, uint4 *__restrict__ dst, uint64_t n) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 }  // namespace
+
+hipError_t pi_launch_copy16(const void *src, void *dst, uint64_t words, hipStream_t s) {
+    if (!words) return hipSuccess;
+    hipLaunchKernelGGL(k_copy16, dim3(8192), dim3(256), 0, s, (const uint4 *)src, (uint4 *)dst, words);
+    return hipGetLastError();
+}
 
 hipError_t pi_launch_repack(const uint8_t *src, uint8_t *dst, const pi_layout &L, hipStream_t s) {
     uint32_t bb = (uint32_t)pi_type_block_bytes(L.type);

@@ -12,6 +12,7 @@
 // amax / min-max encoders that fill every field of the GGML block layouts
 // of quant.rs:102-359.
 #include "pi_common.h"
+#include "pi_detmath.h"
 
 #include <cmath>
 #include <cstring>
@@ -216,6 +217,14 @@ extern "C" int pi_quantize_row(uint32_t type, const float *x, size_t k, uint8_t 
     case PI_TYPE_Q6_K: if (k % 256) return PI_E_INVALID; quant_q6_k(x, k, out); return PI_OK;
     default: return PI_E_UNSUPPORTED;
     }
+}
+
+extern "C" int pi_synth_kv_normal(uint64_t seed, uint32_t lh, uint32_t p0, uint32_t n, uint32_t dh, float *k,
+                                  float *v) {
+    if ((n && (!k || !v)) || dh == 0 || dh > 256) return PI_E_INVALID;
+    for (uint32_t p = 0; p < n; p++)
+        for (uint32_t d = 0; d < dh; d++) pi_kv_normal(seed, lh, p0 + p, d, k + (size_t)p * dh + d, v + (size_t)p * dh + d);
+    return PI_OK;
 }
 
 extern "C" int pi_synth_normal(uint64_t seed, size_t n, float mean, float std_, float *out) {

@@ -40,13 +40,13 @@ EXPORTS = [
     "pi_hip_supports", "pi_hip_selftest", "pi_hip_matvec", "pi_hip_clear_weight_cache",
     "pi_hip_upload", "pi_hip_tensor_free", "pi_hip_tensor_bytes", "pi_hip_gemv_dev",
     "pi_hip_gemv_q8_dev", "pi_hip_time_gemv", "pi_hip_q8_quantize_dev", "pi_hip_dev_alloc",
-    "pi_hip_dev_free", "pi_hip_copy_h2d", "pi_hip_copy_d2h", "pi_hip_set_stream", "pi_hip_synchronize",
+    "pi_hip_dev_free", "pi_hip_copy_h2d", "pi_hip_copy_d2h", "pi_hip_copy_d2d", "pi_hip_set_stream", "pi_hip_synchronize",
     "pi_hip_q8_quantize", "pi_hip_block_sums", "pi_hip_fail_next",
     "pi_hip_model_bind", "pi_hip_forward", "pi_hip_logits", "pi_hip_argmax", "pi_hip_generate",
     "pi_hip_kv_write", "pi_hip_kv_read", "pi_hip_kv_fill_normal", "pi_hip_kv_set_tokens",
     "pi_hip_request_stop", "pi_hip_clear_stop", "pi_hip_use_graphs", "pi_hip_last_decode_us",
     "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
-    "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor",
+    "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor", "pi_synth_kv_normal",
     "pi_quantize_row",
 ]
 
@@ -119,6 +119,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_hip_dev_free": (None, [vp, vp]),
         "pi_hip_copy_h2d": (i32, [vp, vp, vp, sz]),
         "pi_hip_copy_d2h": (i32, [vp, vp, vp, sz]),
+        "pi_hip_copy_d2d": (i32, [vp, vp, vp, sz]),
         "pi_hip_set_stream": (i32, [vp, vp]),
         "pi_hip_synchronize": (i32, [vp]),
         "pi_hip_q8_quantize": (i32, [vp, vp, sz, i32, vp, vp, vp]),
@@ -145,6 +146,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_synth_q4k_random": (i32, [u64, sz, sz, f32, f32, vp]),
         "pi_synth_q6k_random": (i32, [u64, sz, sz, f32, f32, vp]),
         "pi_synth_normal": (i32, [u64, sz, f32, f32, vp]),
+        "pi_synth_kv_normal": (i32, [u64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
         "pi_synth_tensor": (i32, [u64, u32, sz, sz, f32, f32, vp, i32]),
         "pi_quantize_row": (i32, [u32, vp, sz, vp]),
     }
@@ -195,6 +197,15 @@ def synth_normal(seed: int, n: int, mean=0.0, std=1.0) -> np.ndarray:
     out = np.empty(n, np.float32)
     _check(load_library().pi_synth_normal(seed, n, mean, std, _ptr(out)), None)
     return out
+
+
+def synth_kv_normal(seed: int, lh: int, p0: int, n: int, dh: int = 64):
+    """Host copy of what HipEngine.kv_fill_normal writes: (k, v), [n][dh] each,
+    for positions p0..p0+n-1 of layer-major kv head lh."""
+    k = np.empty((n, dh), np.float32)
+    v = np.empty((n, dh), np.float32)
+    _check(load_library().pi_synth_kv_normal(seed, lh, p0, n, dh, _ptr(k), _ptr(v)), None)
+    return k, v
 
 
 def synth_tensor(seed: int, t: int, rows: int, k: int, mean=0.0, std=0.02, threads: int | None = None) -> np.ndarray:
@@ -332,6 +343,10 @@ class HipBackend:
         buf = self.alloc(a.nbytes)
         self.check(self.lib.pi_hip_copy_h2d(self.ctx, buf.ptr, _ptr(a), a.nbytes))
         return buf
+
+    def copy_d2d(self, dst: "DevBuf", src: "DevBuf", nbytes: int) -> None:
+        assert nbytes <= dst.nbytes and nbytes <= src.nbytes
+        self.check(self.lib.pi_hip_copy_d2d(self.ctx, dst.ptr, src.ptr, nbytes))
 
     def set_stream(self, stream_ptr: int | None) -> None:
         self.check(self.lib.pi_hip_set_stream(self.ctx, stream_ptr or None))

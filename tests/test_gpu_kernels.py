@@ -149,3 +149,13 @@ def test_matvec_rejects_bad_shapes(pih, backend):
         backend.matvec(Q4_K, w, 512, np.ones(512, np.float32), 4)
     with pytest.raises(pih.PiError):
         backend.matvec(0, w, 256, np.ones(256, np.float32), 4)
+
+
+@pytest.mark.parametrize("n", [1 << 20, 4096 * 16 + 5, 7])
+def test_copy_d2d(pih, backend, n):
+    """Copy kernel for the 16-byte bulk plus a runtime copy of the tail."""
+    src = np.random.default_rng(n).integers(0, 256, n, dtype=np.uint8)
+    s, d = backend.to_device(src), backend.alloc(n)
+    backend.copy_d2d(d, s, n)
+    backend.synchronize()
+    assert np.array_equal(d.to_host(np.uint8), src)
