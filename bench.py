@@ -147,7 +147,12 @@ def main():
     ap.add_argument("--no-graphs", action="store_true", help="launch kernels one by one (for profilers)")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill and long-context sections")
     ap.add_argument("--profile-gemv", action="store_true", help="GEMV launches and a device copy only")
+    ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV measurements")
+    ap.add_argument("--skip", default="", help="comma list of sections to leave out: gemv,decode,prefill,long,cpu")
     args = ap.parse_args()
+    skip = set(x for x in args.skip.split(",") if x)
+    args.no_gemv |= "gemv" in skip
+    args.no_cpu_baseline |= "cpu" in skip
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py runs on one MI355X only: multi-GPU runs are not part of this build "
               "(the sharding plan is described in DESIGN.md)", file=sys.stderr)
@@ -161,10 +166,12 @@ def main():
         return
 
     # -- roofline: dominant kernel, config-1 shape, HBM-cold -----------------
-    q4k_us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
+    q4k_us = q6k_us = float("nan")
+    if not args.no_gemv:
+        q4k_us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
+        q6k_us = time_gemv(b, pih.Q6_K, Q6K_ROWS, Q6K_K, pih.synth_q6k_random, 3, 30)
     q4k_gbs = Q4K_LAUNCH_BYTES / (q4k_us * 1e-6) / 1e9
     log(f"Q4_K GEMV {Q4K_ROWS}x{Q4K_K}: {q4k_us:.2f} us/launch, {q4k_gbs:.0f} GB/s")
-    q6k_us = time_gemv(b, pih.Q6_K, Q6K_ROWS, Q6K_K, pih.synth_q6k_random, 3, 30)
     q6k_gbs = Q6K_LAUNCH_BYTES / (q6k_us * 1e-6) / 1e9
     log(f"Q6_K GEMV {Q6K_ROWS}x{Q6K_K}: {q6k_us:.2f} us/launch, {q6k_gbs:.0f} GB/s")
 
@@ -175,14 +182,19 @@ def main():
     log(f"model synthesized in {time.time() - t0:.1f}s; {model.weight_bytes_per_token()} weight bytes/token")
     prompt = splitmix_ids(PROMPT_SEED, N_PROMPT, spec.n_vocab)
     n_tokens = args.steps + 1
-    eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + max(n_tokens, args.warmup + 1) + 8)
-    eng.generate(prompt, args.warmup + 1)
-    b.synchronize()
-    ids, st = eng.generate(prompt, n_tokens)
-    b.synchronize()
+    if "decode" in skip:
+        ids, st = [], {"gen_tokens": 1, "gen_ms": float("nan"), "stop": "skipped", "prefill_ms": 0.0,
+                       "prefill_cached_tokens": 0}
+        eng = None
+    else:
+        eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + max(n_tokens, args.warmup + 1) + 8)
+        eng.generate(prompt, args.warmup + 1)
+        b.synchronize()
+        ids, st = eng.generate(prompt, n_tokens)
+        b.synchronize()
     fwd = max(st["gen_tokens"] - 1, 1)
     tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
-    dev_us = eng.last_decode_us()
+    dev_us = eng.last_decode_us() if eng else float("nan")
     wbytes = model.weight_bytes_per_token()
     log(f"decode: {st['gen_tokens']} tokens in {st['gen_ms']:.1f} ms ({tps:.1f} tok/s), "
         f"device {dev_us:.1f} us/forward, stop={st['stop']}, prefill {st['prefill_ms']:.1f} ms "
@@ -191,13 +203,14 @@ def main():
     match = None
     if golden.exists():
         g = json.loads(golden.read_text())
-        if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED:
+        if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED and len(ids) >= g["n_gen"]:
             match = ids[: g["n_gen"]] == g["gen_ids"]
 
     prefill = long_ctx = None
-    if not args.no_extra:
+    if not args.no_extra and "prefill" not in skip:
         prefill = bench_prefill(b, model, spec)
         log(f"prefill: {prefill}")
+    if not args.no_extra and "long" not in skip:
         long_ctx = [bench_long_context(b, model, n, 16, wbytes) for n in (4096, 16384)]
         log(f"long context: {long_ctx}")
 

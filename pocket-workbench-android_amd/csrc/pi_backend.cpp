@@ -455,7 +455,7 @@ pig::MatSet mset(std::initializer_list<const pi_tensor *> ts) {
 int build_mega(pi_ctx *c, Engine &e) {
     e.mega_ok = false;
     const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
-    if (e.n_embd % 128 || e.n_embd / 32 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64) return PI_OK;
+    if (e.n_embd % 128 || e.n_embd / 16 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64) return PI_OK;
     int maxlds = 0;
     if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;
     e.mega_lds = pi_mega_lds_bytes(e.n_embd, e.n_ff, e.n_ctx);
@@ -567,16 +567,32 @@ hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, u
         float *kc = e.kc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
         float *vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
         K(pi_pf_norm_q8(e.pfX, L.attn_norm, e.n_embd, e.eps, ntok, A, s));
-        K(pi_pf_gemm(pfmat(L.q), A, ntok, e.pfQ, false, s));
-        K(pi_pf_gemm(pfmat(L.k), A, ntok, e.pfK, false, s));
-        K(pi_pf_gemm(pfmat(L.v), A, ntok, e.pfV, false, s));
+        {
+            const pi_pf_mat m[3] = {pfmat(L.q), pfmat(L.k), pfmat(L.v)};
+            float *const o[3] = {e.pfQ, e.pfK, e.pfV};
+            if (m[2].L.type == m[0].L.type && m[1].L.type == m[0].L.type) {
+                K(pi_pf_gemm_multi(m, o, 3, A, ntok, false, s));
+            } else {
+                K(pi_pf_gemm_multi(m, o, m[1].L.type == m[0].L.type ? 2 : 1, A, ntok, false, s));
+                if (m[1].L.type != m[0].L.type) K(pi_pf_gemm(m[1], A, ntok, e.pfK, false, s));
+                K(pi_pf_gemm(m[2], A, ntok, e.pfV, false, s));
+            }
+        }
         K(pi_pf_rope_kv(e.pfQ, e.pfK, e.pfV, e.cos_tab, e.sin_tab, pos0, ntok, e.n_head, e.n_kv, e.n_rot / 2, kc, vc,
                         e.n_ctx, s));
         K(pi_pf_attn(e.pfQ, kc, vc, pos0, ntok, e.n_head, e.n_kv, e.n_ctx, scale, A, s));
         K(pi_pf_gemm(pfmat(L.o), A, ntok, e.pfX, true, s));
         K(pi_pf_norm_q8(e.pfX, L.ffn_norm, e.n_embd, e.eps, ntok, A, s));
-        K(pi_pf_gemm(pfmat(L.gate), A, ntok, e.pfG, false, s));
-        K(pi_pf_gemm(pfmat(L.up), A, ntok, e.pfU, false, s));
+        {
+            const pi_pf_mat m[2] = {pfmat(L.gate), pfmat(L.up)};
+            float *const o[2] = {e.pfG, e.pfU};
+            if (m[1].L.type == m[0].L.type) {
+                K(pi_pf_gemm_multi(m, o, 2, A, ntok, false, s));
+            } else {
+                K(pi_pf_gemm(m[0], A, ntok, e.pfG, false, s));
+                K(pi_pf_gemm(m[1], A, ntok, e.pfU, false, s));
+            }
+        }
         K(pi_pf_swiglu_q8(e.pfG, e.pfU, ntok, e.n_ff, A, s));
         K(pi_pf_gemm(pfmat(L.down), A, ntok, e.pfX, true, s));
     }

@@ -98,24 +98,143 @@ __device__ __forceinline__ void q8_lane(const float (&v)[32], uint32_t *qw, floa
 
 // The same rule for a block spread over 32 consecutive lanes (lane j of the
 // half-wave holds element j); used where the values already live in lanes.
-__device__ __forceinline__ void q8_block32(float v, int j, int8_t *qout, float *dout, int32_t *sout, bool store) {
+// Returns this lane's quant; d and the block sum are returned in every lane.
+__device__ __forceinline__ int q8_block32_core(float v, float &dd, int &sum) {
     float a = (v == v) ? fabsf(v) : 0.0f;
 #pragma unroll
     for (int off = 16; off; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
-    const float dd = a / 127.0f;
+    dd = a / 127.0f;
     const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
     float r = roundf(v * inv);
     if (r < -127.0f) r = -127.0f;
     if (r > 127.0f) r = 127.0f;
     const int iv = (r != r) ? 0 : (int)r;
-    if (store) qout[j] = (int8_t)iv;
     int s = iv;
 #pragma unroll
     for (int off = 16; off; off >>= 1) s += __shfl_xor(s, off, 32);
+    sum = s;
+    return iv;
+}
+__device__ __forceinline__ void q8_block32(float v, int j, int8_t *qout, float *dout, int32_t *sout, bool store) {
+    float dd;
+    int s;
+    const int iv = q8_block32_core(v, dd, s);
+    if (store) qout[j] = (int8_t)iv;
     if (store && j == 0) {
         *dout = dd;
         *sout = s;
     }
+}
+
+// The same rule for a block held by two adjacent lanes of a wavefront, 16
+// elements each (the even lane holds elements 0..15).  Both lanes of the
+// pair must call it.  The maximum and the integer sum are exact in any order,
+// so they are formed as trees and completed across the pair.  Returns this
+// half's 4 quant words, and d and the block sum (in both lanes).
+__device__ __forceinline__ void q8_pair_core(const float (&v)[16], uint32_t (&qw)[4], float &dd, int &sum) {
+    float m[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) m[j] = fmaxf(fabsf(v[2 * j]), fabsf(v[2 * j + 1]));   // maxNum: NaN ignored
+#pragma unroll
+    for (int w = 4; w; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) m[j] = fmaxf(m[j], m[j + w]);
+    float amax = fmaxf(m[0], __shfl_xor(m[0], 1, 64));
+    amax = fmaxf(amax, 0.0f);   // all-NaN block: 0
+    dd = amax / 127.0f;
+    const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
+    int iv[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        float r = roundf(v[j] * inv);
+        if (r < -127.0f) r = -127.0f;
+        if (r > 127.0f) r = 127.0f;
+        iv[j] = (r != r) ? 0 : (int)r;
+    }
+#pragma unroll
+    for (int w = 0; w < 4; w++)
+        qw[w] = ((uint32_t)iv[4 * w] & 0xFFu) | (((uint32_t)iv[4 * w + 1] & 0xFFu) << 8) |
+                (((uint32_t)iv[4 * w + 2] & 0xFFu) << 16) | (((uint32_t)iv[4 * w + 3] & 0xFFu) << 24);
+    int t[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) t[j] = iv[2 * j] + iv[2 * j + 1];
+#pragma unroll
+    for (int w = 4; w; w >>= 1)
+#pragma unroll
+        for (int j = 0; j < w; j++) t[j] += t[j + w];
+    sum = t[0] + __shfl_xor(t[0], 1, 64);
+}
+// Writes this half's 4 quant words to qw; the even lane writes d and the sum.
+__device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t half, uint32_t *qw, float *dout,
+                                        int32_t *sout) {
+    uint32_t w4[4];
+    float dd;
+    int sum;
+    q8_pair_core(v, w4, dd, sum);
+#pragma unroll
+    for (int w = 0; w < 4; w++) qw[w] = w4[w];
+    if (half == 0) {
+        *dout = dd;
+        *sout = sum;
+    }
+}
+
+// Calls eat(p[i]) for i = 0..n4-1 in order on a float4 row in LDS.  The
+// reads of the next B float4 are in flight while the current B are used; two
+// named buffers, reads at fixed offsets from one address.  p[n4 .. n4 + B)
+// must be readable LDS (loaded and ignored).
+template <int B, typename F>
+__device__ __forceinline__ void lds_chain4(const float4 *p, uint32_t n4, F &&eat) {
+    uint32_t i = 0;
+    if (n4 >= 2 * B) {
+        float4 a[B], b[B];
+#pragma unroll
+        for (int u = 0; u < B; u++) a[u] = p[u];
+        for (; i + 2 * B <= n4; i += 2 * B) {
+            const float4 *q = p + i;
+#pragma unroll
+            for (int u = 0; u < B; u++) b[u] = q[B + u];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < B; u++) eat(a[u]);
+            __builtin_amdgcn_sched_barrier(0);   // a is dead before its registers are reloaded
+#pragma unroll
+            for (int u = 0; u < B; u++) a[u] = q[2 * B + u];
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < B; u++) eat(b[u]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    for (; i < n4; i++) eat(p[i]);
+}
+
+// acc = fma(v, v, acc) over the row in order: one accumulator of
+// simd::f32_sum_sq (simd.rs:45-64).
+template <int B>
+__device__ __forceinline__ float sumsq_fma_chain(const float4 *p, uint32_t n4) {
+    float acc = 0.0f;
+    lds_chain4<B>(p, n4, [&](const float4 &v) {
+        acc = __builtin_fmaf(v.x, v.x, acc);
+        acc = __builtin_fmaf(v.y, v.y, acc);
+        acc = __builtin_fmaf(v.z, v.z, acc);
+        acc = __builtin_fmaf(v.w, v.w, acc);
+    });
+    return acc;
+}
+
+// ss += v * v over the row in order, product rounded then added: the
+// multi-token loop of model.rs:812-822.
+template <int B>
+__device__ __forceinline__ float sumsq_scalar_chain(const float4 *p, uint32_t n4) {
+    float acc = 0.0f;
+    lds_chain4<B>(p, n4, [&](const float4 &v) {
+        acc += v.x * v.x;
+        acc += v.y * v.y;
+        acc += v.z * v.z;
+        acc += v.w * v.w;
+    });
+    return acc;
 }
 
 // ---------------------------------------------------------------------------

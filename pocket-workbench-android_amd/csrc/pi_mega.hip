@@ -45,6 +45,9 @@ constexpr uint32_t kChunkPad = 68;     // floats per dimension row of a chunk (1
 constexpr uint32_t kRedFloats = 512;   // small LDS scratch
 constexpr uint32_t kStripFloats = MW * 64 * 16;
 
+// Row stride of the transposed x (floats).  The rows are followed by at least
+// 24 more floats of the LDS plan (row padding, then the Q8 activation), which
+// the norm's sum-of-squares chain reads ahead and ignores.
 __host__ __device__ constexpr uint32_t xt_stride(uint32_t ne) { return ne / 8 + 4; }
 __host__ __device__ constexpr uint32_t align16(uint32_t b) { return (b + 15u) & ~15u; }
 __host__ __device__ constexpr uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
@@ -245,6 +248,13 @@ __device__ __forceinline__ void trace_mark(const Cfg &a, uint32_t slot) {
 __device__ __forceinline__ void trace_detail(const Cfg &a, const Run &r, uint32_t k) {
     if (r.detail) trace_mark(a, 3 + 5 * a.n_layer + k);
 }
+// Shader-clock counter at point k of the middle layer (with a real-time point
+// recorded beside it, two of these give the clock the kernel ran at).
+__device__ __forceinline__ void trace_clock(const Cfg &a, const Run &r, uint32_t k) {
+    if (r.detail && a.trace && threadIdx.x == 0)
+        gst(a.trace)[(uint64_t)blockIdx.x * pi_mega_trace_slots(a.n_layer) + 3 + 5 * a.n_layer + k] =
+            __builtin_amdgcn_s_memtime();
+}
 
 // ---------------------------------------------------------------------------
 // RMSNorm (model.rs:777-823) of the x held in xt, then Q8Act::prepare
@@ -253,22 +263,18 @@ __device__ __forceinline__ void trace_detail(const Cfg &a, const Run &r, uint32_
 // (t0 + t1) + (t2 + t3); else the scalar loop of a multi-token batch.
 // out = (x * s) * w.  wr: this thread's 32 norm weights (threads < ne/32).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, const float4 (&wr)[8], bool neon) {
+struct NoMark {
+    __device__ void operator()(uint32_t) const {}
+};
+template <typename Mark = NoMark>
+__device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, const float4 (&wr)[4], bool neon,
+                                        Mark mark = Mark{}) {
     const uint32_t tid = threadIdx.x;
     const uint32_t n4 = ne / 32;  // float4 per transposed row (a multiple of 4: ne % 128 == 0)
     vm_drain();
+    mark(12);
     if (neon) {
-        if (tid < 8) {
-            const float4 *row = reinterpret_cast<const float4 *>(L.xt + tid * L.XT);
-            float acc = 0.0f;
-            lds_fold4<6>(row, n4, [&](const float4 &v) {
-                acc = __builtin_fmaf(v.x, v.x, acc);
-                acc = __builtin_fmaf(v.y, v.y, acc);
-                acc = __builtin_fmaf(v.z, v.z, acc);
-                acc = __builtin_fmaf(v.w, v.w, acc);
-            });
-            L.red[tid] = acc;
-        }
+        if (tid < 8) L.red[tid] = sumsq_fma_chain<6>(reinterpret_cast<const float4 *>(L.xt + tid * L.XT), n4);
         wave_sync();
         if (tid == 0) {
             const float t0 = L.red[0] + L.red[4], t1 = L.red[1] + L.red[5], t2 = L.red[2] + L.red[6],
@@ -295,28 +301,28 @@ __device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, co
         }
     }
     lds_barrier();
+    mark(13);
     const float s = L.red[8];
-    if (tid < ne / 32) {
-        float v[32];
+    if (tid < ne / 16) {
+        // elements 16 * tid + j: xt row j % 8, column 2 * tid + j / 8
+        const uint32_t b = tid >> 1, h = tid & 1u;
+        float v[16];
 #pragma unroll
         for (int c = 0; c < 8; c++) {
-            const float4 t = reinterpret_cast<const float4 *>(L.xt + c * L.XT)[tid];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int e = 8 * q + c;
-                v[e] = comp4(t, q) * s * comp4(wr[e / 4], e % 4);
-            }
+            const float2 t = reinterpret_cast<const float2 *>(L.xt + c * L.XT)[tid];
+            v[c] = t.x * s * comp4(wr[c / 4], c % 4);
+            v[8 + c] = t.y * s * comp4(wr[2 + c / 4], c % 4);
         }
-        q8_lane(v, L.act.qw + 8 * tid, L.act.d + tid, L.act.s + tid);
+        q8_pair(v, h, L.act.qw + 8 * b + 4 * h, L.act.d + b, L.act.s + b);
     }
     lds_barrier();
 }
 
-__device__ __forceinline__ void load_norm_w(const float *w, uint32_t ne, float4 (&wr)[8]) {
-    if (threadIdx.x < ne / 32) {
-        const PI_GLOBAL float4 *w4 = gld(reinterpret_cast<const float4 *>(w + 32 * threadIdx.x));
+__device__ __forceinline__ void load_norm_w(const float *w, uint32_t ne, float4 (&wr)[4]) {
+    if (threadIdx.x < ne / 16) {
+        const PI_GLOBAL float4 *w4 = gld(reinterpret_cast<const float4 *>(w + 16 * threadIdx.x));
 #pragma unroll
-        for (int j = 0; j < 8; j++) wr[j] = w4[j];
+        for (int j = 0; j < 4; j++) wr[j] = w4[j];
     }
 }
 
@@ -430,13 +436,14 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             const bool b_first = gw >= ntA && firstB < ntB;   // B is this wavefront's first work
             if (b_first) prefetch_ring<TB, 1, 1>(SB, firstB, nw, UB, RB);
             else prefetch_ring<TA, 1, 1>(SA, gw, nw, UA, RA);
-            float4 wr[8];
+            float4 wr[4];
             load_norm_w(attn_norm, a.ne, wr);
             lds_barrier();
             if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);
             if (wg_any(!ok, L.vote)) { ok = false; return; }
             trace_detail(a, r, 0);
-            norm_q8(L, a.ne, a.eps, wr, r.neon);
+            trace_clock(a, r, 14);
+            norm_q8(L, a.ne, a.eps, wr, r.neon, [&](uint32_t k) { trace_detail(a, r, k); });
             trace_detail(a, r, 1);
             auto outA = [&](uint32_t m, uint32_t row, float v) {
                 uint64_t *o = m == 0 ? oq : (m == 1 ? okk : ov);
@@ -758,7 +765,7 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
             Ug.load(Rg.base, Rg.lanes, min(lane, Rg.lanes - 1));
             Uu.load(Ru.base, Ru.lanes, min(lane, Ru.lanes - 1));
         }
-        float4 wr[8];
+        float4 wr[4];
         load_norm_w(ffn_norm, a.ne, wr);
         lds_barrier();
         ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
@@ -829,18 +836,19 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
                          [&](uint32_t i, uint32_t bits) { L.hb[i] = __uint_as_float(bits); });
         if (wg_any(!ok, L.vote)) { ok = false; return; }
         trace_detail(a, r, 9);
-        if (threadIdx.x < a.n_ff / 32) {
-            float v[32];
-            const float4 *x4 = reinterpret_cast<const float4 *>(L.hb + 32 * threadIdx.x);
+        for (uint32_t t = threadIdx.x; t < a.n_ff / 16; t += MT) {   // pairs of lanes stay together
+            const uint32_t b = t >> 1, h = t & 1u;
+            float v[16];
+            const float4 *x4 = reinterpret_cast<const float4 *>(L.hb + 16 * t);
 #pragma unroll
-            for (int j4 = 0; j4 < 8; j4++) {
-                const float4 t = x4[j4];
-                v[4 * j4 + 0] = t.x;
-                v[4 * j4 + 1] = t.y;
-                v[4 * j4 + 2] = t.z;
-                v[4 * j4 + 3] = t.w;
+            for (int j4 = 0; j4 < 4; j4++) {
+                const float4 q = x4[j4];
+                v[4 * j4 + 0] = q.x;
+                v[4 * j4 + 1] = q.y;
+                v[4 * j4 + 2] = q.z;
+                v[4 * j4 + 3] = q.w;
             }
-            q8_lane(v, L.act.qw + 8 * threadIdx.x, L.act.d + threadIdx.x, L.act.s + threadIdx.x);
+            q8_pair(v, h, L.act.qw + 8 * b + 4 * h, L.act.d + b, L.act.s + b);
         }
         lds_barrier();
         trace_detail(a, r, 10);
@@ -849,6 +857,7 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
         };
         gemv_ring<T, G, 3>(SD, L, U, R, gw, nw, out);
         trace_detail(a, r, 11);
+        trace_clock(a, r, 15);
     });
     if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
     return ok;
@@ -879,7 +888,7 @@ __device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, c
         Unit<T, 1> U[2];
         TileRef R[2];
         prefetch_ring<T, 1, 2>(SH, gw, nw, U, R);
-        float4 wr[8];
+        float4 wr[4];
         load_norm_w(a.out_norm, a.ne, wr);
         lds_barrier();
         if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);

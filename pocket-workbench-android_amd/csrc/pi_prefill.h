@@ -17,8 +17,10 @@ struct pi_pf_mat {
 };
 
 // Token-major activations of a chunk: row t of a [ntok][n] matrix at t * n.
-// Q8 activations use the Q8Act lane-major layout (quant_int.rs:46-53):
-// q[t * k + j], d[t * k/32 + blk], sum[t * k/32 + blk].
+// Q8 activations (the values of Q8Act, quant_int.rs:17-56) are laid out for
+// the MFMA operand loads: the 8 quants 8*ka..8*ka+7 of 32-element group G of
+// token t at byte ((G * 4 + ka) * 32 + t) * 8; d and the block sum of (G, t)
+// at index G * 32 + t.
 struct pi_pf_q8 {
     int8_t *q;
     float *d;
@@ -35,6 +37,10 @@ hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps,
 // sums of every 32- (Q6_K: 16-) element group, the reference's float
 // epilogue in block order per (row, token).
 hipError_t pi_pf_gemm(const pi_pf_mat &W, pi_pf_q8 act, uint32_t ntok, float *out, bool resid, hipStream_t s);
+// The same for up to 3 matrices of one type and row length sharing the
+// activation, in one launch; out[i] is a [ntok][rows of M[i]] matrix.
+hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg, pi_pf_q8 act, uint32_t ntok,
+                            bool resid, hipStream_t s);
 // RoPE of Q and K of every token (model.rs:953-979) and the K/V rows of
 // positions pos0..pos0+ntok-1 written into this layer's caches (984-992).
 hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *cos_tab, const float *sin_tab,

@@ -32,38 +32,15 @@ __device__ __forceinline__ uint32_t byte16(const uint4 &v, int i) {
     return (w >> (8 * (i & 3))) & 0xFFu;
 }
 
-// Device view of a tiled matrix and the byte offset of chunk j of base
-// block u of row r (bc chunks per base block), or of its f16 field.
+// Device view of a tiled matrix.
 struct WV {
     const uint8_t *w;
     uint32_t rows, upr, rpw, lpt, g, qc, ntiles;
+    uint32_t gmag;        // ceil(2^32 / g) for g > 1: u / g == umulhi(u, gmag) for u < 2^16
     uint64_t tile_bytes;
 };
+__device__ __forceinline__ uint32_t div_g(const WV &W, uint32_t u) { return W.g == 1 ? u : __umulhi(u, W.gmag); }
 
-__device__ __forceinline__ void tile_pos(const WV &W, uint32_t r, uint32_t u, uint64_t &tbase, uint32_t &lanes,
-                                         uint32_t &ln, uint32_t &b) {
-    const uint32_t t = r / W.rpw, rt = r - t * W.rpw;
-    lanes = (t == W.ntiles - 1) ? (W.rows - t * W.rpw) * W.upr : W.lpt;
-    const uint32_t unit = u / W.g;
-    b = u - unit * W.g;
-    ln = rt * W.upr + unit;
-    tbase = (uint64_t)t * W.tile_bytes;
-}
-__device__ __forceinline__ const uint8_t *chunk_at(const WV &W, uint32_t r, uint32_t u, uint32_t j, uint32_t bc) {
-    uint64_t tb;
-    uint32_t lanes, ln, b;
-    tile_pos(W, r, u, tb, lanes, ln, b);
-    return W.w + tb + ((uint64_t)(b * bc + j) * lanes + ln) * 16u;
-}
-__device__ __forceinline__ float dfield_at(const WV &W, uint32_t r, uint32_t u) {
-    uint64_t tb;
-    uint32_t lanes, ln, b;
-    tile_pos(W, r, u, tb, lanes, ln, b);
-    const PI_GLOBAL uint16_t *p =
-        gld(reinterpret_cast<const uint16_t *>(W.w + tb + (uint64_t)lanes * W.qc * 16u + ((uint64_t)b * lanes + ln) * 2u));
-    return h2f(*p);
-}
-__device__ __forceinline__ uint2 ld8(const uint8_t *p) { return *gld(reinterpret_cast<const uint2 *>(p)); }
 __device__ __forceinline__ uint4 ld16(const uint8_t *p) { return *gld(reinterpret_cast<const uint4 *>(p)); }
 
 __device__ __forceinline__ v4i mfma16(long a, long b) {
@@ -72,154 +49,397 @@ __device__ __forceinline__ v4i mfma16(long a, long b) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM: a wavefront owns 16 rows x 16 tokens.  Lane l: A row r0 + l%16 with
-// group elements 8*(l/16)..+7; B (and D) token 16*th + l%16; D rows
-// r0 + 4*(l/16) + i, i = 0..3.
+// GEMM.  A workgroup of four wavefronts owns 16 rows of one matrix and 16
+// tokens of the chunk.  Every (row, token) output is 0 + t_0 + t_1 + ... in
+// the reference's term order (one term per 32-element group; Q6_K one per
+// 16-element group in (half, g, s) order).  The terms are formed in phases
+// of 16: in each phase wavefront w forms terms 4w..4w+3 for all 256
+// (row, token) pairs - one int8 MFMA (lane l: A row r0 + l%16 with group
+// elements 8*(l/16)..+7; B token l%16; D rows 4*(l/16)+i) and the float
+// term per pair - into an LDS plane; after a barrier, thread p adds the
+// phase's terms of pair p in order.  The weight chunks a phase needs are
+// staged into LDS by the whole workgroup (whole 16-byte chunks, one phase
+// ahead), the activation operands come in token-contiguous runs, and the
+// per-row constants of the terms (f16 scales, 6-bit sub-block scales/mins,
+// Q6_K d*scale) are decoded once into LDS.  Two planes and two weight
+// buffers alternate: one barrier per phase.
 // ---------------------------------------------------------------------------
-template <uint32_t T>
-__global__ __launch_bounds__(256) void k_pf_gemm(WV W, const int8_t *__restrict__ aq, const float *__restrict__ ad,
-                                                 const int32_t *__restrict__ as, uint32_t k, uint32_t ntok,
-                                                 float *__restrict__ out, uint32_t ld, int resid) {
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t wv = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t r0 = (wv >> 1) * 16, th = wv & 1u;
-    if (r0 >= W.rows || th * 16 >= ntok) return;
-    const uint32_t ka = lane >> 4, li = lane & 15u;
-    const uint32_t ra = min(r0 + li, W.rows - 1);
-    const uint32_t n = th * 16 + li;
-    const bool n_ok = n < ntok;
-    const uint32_t nn = n_ok ? n : 0u;
-    const uint32_t nb32 = k / 32;
-    const int8_t *arow = aq + (uint64_t)nn * k;
-    const PI_GLOBAL float *adr = gld(ad + (uint64_t)nn * nb32);
-    const PI_GLOBAL int32_t *asr = gld(as + (uint64_t)nn * nb32);
-    uint32_t rd[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) rd[i] = min(r0 + 4 * ka + (uint32_t)i, W.rows - 1);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+constexpr uint32_t kPfRows = 16;
+constexpr uint32_t kPfThreads = 256;
+constexpr uint32_t kPfPhase = 16;                   // terms per row per phase
+constexpr uint32_t kPfTermsPerWave = kPfPhase / 4;
+constexpr uint32_t kPfTokPad = 20;                  // floats per row of a term plane (16 tokens + 4)
+constexpr uint32_t kPfPlane = kPfRows * kPfTokPad;  // floats per term plane: [row][token]
+constexpr uint32_t kPfMaxSeg = 3;
 
-    if constexpr (T == PI_TYPE_Q4_K) {
-        const uint32_t nblk = k / 256;
-        for (uint32_t u = 0; u < nblk; u++) {
-            uint4 hdr[4];
+// Row r of a tiled matrix: its tile, the tile's lane count and the lane of
+// the row's first unit.
+struct RowPos {
+    const uint8_t *tile;
+    uint32_t lanes, ln0;
+};
+__device__ __forceinline__ RowPos row_pos(const WV &W, uint32_t r) {
+    const uint32_t t = r / W.rpw, rt = r - t * W.rpw;
+    RowPos p;
+    p.tile = W.w + (uint64_t)t * W.tile_bytes;
+    p.lanes = (t == W.ntiles - 1) ? (W.rows - t * W.rpw) * W.upr : W.lpt;
+    p.ln0 = rt * W.upr;
+    return p;
+}
+
+struct PfSegs {
+    WV W[kPfMaxSeg];
+    float *out[kPfMaxSeg];
+    uint32_t wg_end[kPfMaxSeg];   // cumulative workgroup counts
+    uint32_t nseg;
+};
+
+// Offset of the 8 quants 8*ka..+7 of group G of token t in a prefill Q8 buffer.
+__device__ __forceinline__ uint64_t pfq_off(uint32_t G, uint32_t ka, uint32_t t) {
+    return (((uint64_t)G * 4 + ka) * PI_PF_MAX_TOK + t) * 8;
+}
+// Stores the Q8 of half hh of block b of token t (q8_pair_core results).
+__device__ __forceinline__ void pf_store_pair(pi_pf_q8 o, uint32_t t, uint32_t b, uint32_t hh, const uint32_t (&w4)[4],
+                                              float dd, int sum) {
+    *reinterpret_cast<uint2 *>(o.q + pfq_off(b, 2 * hh, t)) = make_uint2(w4[0], w4[1]);
+    *reinterpret_cast<uint2 *>(o.q + pfq_off(b, 2 * hh + 1, t)) = make_uint2(w4[2], w4[3]);
+    if (hh == 0) {
+        o.d[b * PI_PF_MAX_TOK + t] = dd;
+        o.s[b * PI_PF_MAX_TOK + t] = sum;
+    }
+}
+__device__ __forceinline__ float f4(const float4 &v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
+
+template <uint32_t T>
+struct PfLds;
+// Q4_K: d, dmin per (block, row); s, m per (block, sub-block, row).
+template <>
+struct PfLds<PI_TYPE_Q4_K> {
+    static constexpr uint32_t floats_per_block = 16 * 2 + 8 * 16 * 2;
+};
+// Q6_K: d * scale per (block, 16-group, row).
+template <>
+struct PfLds<PI_TYPE_Q6_K> {
+    static constexpr uint32_t floats_per_block = 16 * 16;
+};
+// Q4_0 / Q8_0: d per (block, row).
+template <>
+struct PfLds<PI_TYPE_Q4_0> {
+    static constexpr uint32_t floats_per_block = 16;
+};
+template <>
+struct PfLds<PI_TYPE_Q8_0> {
+    static constexpr uint32_t floats_per_block = 16;
+};
+
+// Decodes the epilogue constants of rows r0..r0+15 into cst (all loads of a
+// round are issued before any is used).
+template <uint32_t T>
+__device__ __forceinline__ void decode_consts(const WV &W, uint32_t r0, uint32_t nb, float *cst) {
+    constexpr uint32_t R = (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) ? 2u : 24u;   // entries per thread per round
+    const uint32_t tid = threadIdx.x, ne = nb * kPfRows;
+    for (uint32_t base = 0; base < ne; base += kPfThreads * R) {
+        if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) {
+            uint4 h[R];
+            float dv[R];
 #pragma unroll
-            for (int i = 0; i < 4; i++) hdr[i] = ld16(chunk_at(W, rd[i], u, 0, 9));
-            uint2 qa[4];
-#pragma unroll
-            for (int g = 0; g < 4; g++) qa[g] = ld8(chunk_at(W, ra, u, 1 + 2 * g + (ka >> 1), 9) + 8 * (ka & 1));
-            long bq[8];
-#pragma unroll
-            for (int sb = 0; sb < 8; sb++) bq[sb] = *gld(reinterpret_cast<const long *>(arow + u * 256 + sb * 32 + 8 * ka));
-#pragma unroll
-            for (int sb = 0; sb < 8; sb++) {
-                const int g = sb >> 1, h = sb & 1;
-                const uint32_t lo = h ? (qa[g].x >> 4) & 0x0F0F0F0Fu : qa[g].x & 0x0F0F0F0Fu;
-                const uint32_t hi = h ? (qa[g].y >> 4) & 0x0F0F0F0Fu : qa[g].y & 0x0F0F0F0Fu;
-                const v4i c = mfma16(pack2(lo, hi), bq[sb]);
-                const float da = adr[u * 8 + sb];
-                const float asf = (float)asr[u * 8 + sb];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float d = h2f(hdr[i].x), dmin = h2f(hdr[i].x >> 16);
-                    uint32_t s, m;  // get_scale_min_k4 on the 12 scale bytes (bytes 4..15)
-                    if (sb < 4) {
-                        s = byte16(hdr[i], 4 + sb) & 63u;
-                        m = byte16(hdr[i], 4 + sb + 4) & 63u;
-                    } else {
-                        s = (byte16(hdr[i], 4 + sb + 4) & 0xFu) | ((byte16(hdr[i], 4 + sb - 4) >> 6) << 4);
-                        m = (byte16(hdr[i], 4 + sb + 4) >> 4) | ((byte16(hdr[i], 4 + sb) >> 6) << 4);
-                    }
-                    const float term = d * da * (float)s * (float)c[i] - da * dmin * (float)m * asf;
-                    acc[i] += term;
+            for (uint32_t j = 0; j < R; j++) {
+                const uint32_t p = min(base + tid + kPfThreads * j, ne - 1), i = p % kPfRows, u = p / kPfRows;
+                const RowPos rp = row_pos(W, min(r0 + i, W.rows - 1));
+                if constexpr (T == PI_TYPE_Q4_K) {
+                    h[j] = ld16(rp.tile + (uint64_t)(rp.ln0 + u) * 16u);
+                } else {
+                    h[j] = ld16(rp.tile + (uint64_t)(12u * rp.lanes + rp.ln0 + u) * 16u);
+                    dv[j] = h2f(*gld(reinterpret_cast<const uint16_t *>(rp.tile + (uint64_t)rp.lanes * W.qc * 16u +
+                                                                        (uint64_t)(rp.ln0 + u) * 2u)));
                 }
             }
-        }
-    } else if constexpr (T == PI_TYPE_Q6_K) {
-        const uint32_t nblk = k / 256;
-        for (uint32_t u = 0; u < nblk; u++) {
-            uint4 sc4[4];
-            float d6[4];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                sc4[i] = ld16(chunk_at(W, rd[i], u, 12, 13));
-                d6[i] = dfield_at(W, rd[i], u);
-            }
-            long bq[8];
+            for (uint32_t j = 0; j < R; j++) {
+                const uint32_t p = base + tid + kPfThreads * j;
+                if (p >= ne) break;
+                const uint32_t i = p % kPfRows, u = p / kPfRows;
+                float *c = cst + (uint64_t)u * PfLds<T>::floats_per_block;
+                if constexpr (T == PI_TYPE_Q4_K) {
+                    c[i] = h2f(h[j].x);
+                    c[16 + i] = h2f(h[j].x >> 16);
 #pragma unroll
-            for (int j = 0; j < 8; j++) bq[j] = *gld(reinterpret_cast<const long *>(arow + u * 256 + j * 32 + 8 * ka));
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-                const uint2 ql0 = ld8(chunk_at(W, ra, u, half * 4 + (ka >> 1), 13) + 8 * (ka & 1));
-                const uint2 ql1 = ld8(chunk_at(W, ra, u, half * 4 + 2 + (ka >> 1), 13) + 8 * (ka & 1));
-                const uint2 qh = ld8(chunk_at(W, ra, u, 8 + half * 2 + (ka >> 1), 13) + 8 * (ka & 1));
-#pragma unroll
-                for (int g = 0; g < 2; g++) {
-                    const bool mine = (ka >> 1) == (uint32_t)g;   // this lane's 8 elements are in group g
-#pragma unroll
-                    for (int s = 0; s < 4; s++) {
-                        const uint2 qlw = (s & 1) ? ql1 : ql0;
-                        uint32_t w6[2];
-#pragma unroll
-                        for (int c = 0; c < 2; c++) {
-                            const uint32_t l4 = c ? qlw.y : qlw.x, h2 = c ? qh.y : qh.x;
-                            const uint32_t nib = s < 2 ? (l4 & 0x0F0F0F0Fu) : ((l4 >> 4) & 0x0F0F0F0Fu);
-                            const uint32_t q = nib | (((h2 >> (2 * s)) & 0x03030303u) << 4);   // 0..63 per byte
-                            const uint32_t x = q ^ 0x20202020u;                               // q - 32 in 6 bits
-                            w6[c] = x | ((x & 0x20202020u) * 6u);                              // sign-extend to 8
+                    for (int sb = 0; sb < 8; sb++) {
+                        uint32_t sv, mv;   // get_scale_min_k4 on the 12 scale bytes (bytes 4..15)
+                        if (sb < 4) {
+                            sv = byte16(h[j], 4 + sb) & 63u;
+                            mv = byte16(h[j], 4 + sb + 4) & 63u;
+                        } else {
+                            sv = (byte16(h[j], 4 + sb + 4) & 0xFu) | ((byte16(h[j], 4 + sb - 4) >> 6) << 4);
+                            mv = (byte16(h[j], 4 + sb + 4) >> 4) | ((byte16(h[j], 4 + sb) >> 6) << 4);
                         }
-                        const long A = mine ? pack2(w6[0], w6[1]) : 0L;
-                        const v4i c = mfma16(A, bq[4 * half + s]);
-                        const float da = adr[u * 8 + 4 * half + s];
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const float scale = (float)(int8_t)byte16(sc4[i], half * 8 + g + 2 * s);
-                            const float term = d6[i] * scale * da * (float)c[i];
-                            acc[i] += term;
-                        }
+                        c[32 + sb * 16 + i] = (float)sv;
+                        c[32 + 128 + sb * 16 + i] = (float)mv;
                     }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < 16; q++) c[q * 16 + i] = dv[j] * (float)(int8_t)byte16(h[j], q);
                 }
             }
-        }
-    } else if constexpr (T == PI_TYPE_Q8_0) {
-        const uint32_t nblk = k / 32;
-        for (uint32_t u = 0; u < nblk; u++) {
-            const uint2 w8 = ld8(chunk_at(W, ra, u, ka >> 1, 2) + 8 * (ka & 1));
-            const long bq = *gld(reinterpret_cast<const long *>(arow + u * 32 + 8 * ka));
-            const v4i c = mfma16(pack2(w8.x, w8.y), bq);
-            const float da = adr[u];
+        } else {
+            uint32_t hv[R];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float term = dfield_at(W, rd[i], u) * da * (float)c[i];
-                acc[i] += term;
+            for (uint32_t j = 0; j < R; j++) {
+                const uint32_t p = min(base + tid + kPfThreads * j, ne - 1), i = p % kPfRows, u = p / kPfRows;
+                const RowPos rp = row_pos(W, min(r0 + i, W.rows - 1));
+                const uint32_t unit = div_g(W, u), b = u - unit * W.g;
+                hv[j] = *gld(reinterpret_cast<const uint16_t *>(rp.tile + (uint64_t)rp.lanes * W.qc * 16u +
+                                                                (uint64_t)(b * rp.lanes + rp.ln0 + unit) * 2u));
             }
-        }
-    } else {  // Q4_0: lo nibbles -> elements 0..15, hi -> 16..31
-        const uint32_t nblk = k / 32;
-        for (uint32_t u = 0; u < nblk; u++) {
-            const uint2 raw = ld8(chunk_at(W, ra, u, 0, 1) + 8 * (ka & 1));
-            const uint32_t sh = (ka >> 1) * 4;
-            const long A = pack2((raw.x >> sh) & 0x0F0F0F0Fu, (raw.y >> sh) & 0x0F0F0F0Fu);
-            const long bq = *gld(reinterpret_cast<const long *>(arow + u * 32 + 8 * ka));
-            const v4i c = mfma16(A, bq);
-            const float da = adr[u];
-            const float asf = (float)asr[u];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float term = dfield_at(W, rd[i], u) * da * ((float)c[i] - 8.0f * asf);
-                acc[i] += term;
+            for (uint32_t j = 0; j < R; j++) {
+                const uint32_t p = base + tid + kPfThreads * j;
+                if (p >= ne) break;
+                cst[(p / kPfRows) * PfLds<T>::floats_per_block + p % kPfRows] = h2f(hv[j]);
             }
         }
     }
-    if (n_ok) {
+}
+
+// Runs use(buffer, i) for i = 0..n-1 in order with the loads of the next
+// P - 1 steps in flight: P buffers in registers, the inner loop unrolled so
+// each keeps its registers; loads past the end repeat step n - 1.  middle()
+// runs after the first P loads are issued; its false return ends the run.
+template <int P, typename L, typename U, typename M>
+__device__ __forceinline__ void ring_run(uint32_t n, L &&load, U &&use, M &&middle) {
+    using Buf = decltype(load(0u));
+    Buf R[P];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t r = r0 + 4 * ka + (uint32_t)i;
-            if (r < W.rows) {
-                float *o = out + (uint64_t)n * ld + r;
-                const float v = 0.0f + acc[i];
-                *o = resid ? *o + v : v;
+    for (int k = 0; k < P; k++) R[k] = load(min((uint32_t)k, n - 1));
+    if (!middle()) return;
+    for (uint32_t i0 = 0; i0 < n; i0 += P) {
+#pragma unroll
+        for (int k = 0; k < P; k++) {
+            if (i0 + k < n) {
+                use(R[k], i0 + k);
+                R[k] = load(min(i0 + k + P, n - 1));
             }
         }
+    }
+}
+
+// Weight chunks staged per phase (16-byte pieces): blocks per phase, pieces
+// per row and the LDS row stride in pieces (odd multiples of 4 dwords keep
+// the 16 rows of an MFMA read on distinct banks).
+template <uint32_t T> struct PfStage;
+template <> struct PfStage<PI_TYPE_Q4_K> { static constexpr uint32_t PB = 2, PPR = 16, WS = 17; };   // qs chunks 1..8
+template <> struct PfStage<PI_TYPE_Q6_K> { static constexpr uint32_t PB = 1, PPR = 12, WS = 13; };   // ql, qh chunks 0..11
+template <> struct PfStage<PI_TYPE_Q8_0> { static constexpr uint32_t PB = 16, PPR = 32, WS = 33; };
+template <> struct PfStage<PI_TYPE_Q4_0> { static constexpr uint32_t PB = 16, PPR = 16, WS = 17; };
+
+// Activation operands of one term for one lane.
+struct TermAct {
+    uint2 b;   // 8 activation quants
+    float da;
+    int as;
+};
+
+template <uint32_t T>
+__global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *__restrict__ aq,
+                                                         const float *__restrict__ ad, const int32_t *__restrict__ as,
+                                                         uint32_t k, uint32_t ntok, int resid) {
+    using ST = PfStage<T>;
+    constexpr uint32_t PIECES = kPfRows * ST::PPR;                       // per phase
+    constexpr uint32_t PPT = (PIECES + kPfThreads - 1) / kPfThreads;    // pieces per thread
+    extern __shared__ __align__(16) float lds[];
+    const uint32_t wg = blockIdx.x;
+    const uint32_t seg = (S.nseg > 1 && wg >= S.wg_end[0]) ? ((S.nseg > 2 && wg >= S.wg_end[1]) ? 2u : 1u) : 0u;
+    const WV W = seg == 0 ? S.W[0] : (seg == 1 ? S.W[1] : S.W[2]);
+    float *const out = seg == 0 ? S.out[0] : (seg == 1 ? S.out[1] : S.out[2]);
+    const uint32_t wg0 = seg == 0 ? 0u : (seg == 1 ? S.wg_end[0] : S.wg_end[1]);
+    const uint32_t nth = (ntok + 15) / 16;
+    const uint32_t rg = (wg - wg0) / nth, th = (wg - wg0) - rg * nth;
+    const uint32_t r0 = rg * kPfRows;
+    const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+    const uint32_t ka = lane >> 4, li = lane & 15u;
+    constexpr bool KQ = T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K;
+    const uint32_t nb = k / (KQ ? 256u : 32u);
+    const uint32_t tpr = T == PI_TYPE_Q6_K ? 16 * nb : (T == PI_TYPE_Q4_K ? 8 * nb : nb);   // terms per row
+    const uint32_t nph = (tpr + kPfPhase - 1) / kPfPhase;
+    float *cst = lds;
+    float *pl0 = lds + (((uint64_t)nb * PfLds<T>::floats_per_block + 3) & ~3ull);
+    float *pl1 = pl0 + kPfPhase * kPfPlane;
+    uint4 *wb0 = reinterpret_cast<uint4 *>(pl1 + kPfPhase * kPfPlane);
+    uint4 *wb1 = wb0 + kPfRows * ST::WS;
+
+    // ---- staging: this thread's pieces -----------------------------------
+    struct Piece {
+        const uint8_t *tile;
+        uint32_t lanes, ln0, q;   // q: piece index within a phase (PIECES: none)
+    };
+    Piece pc[PPT];
+#pragma unroll
+    for (uint32_t j = 0; j < PPT; j++) {
+        const uint32_t q = tid + kPfThreads * j;
+        const uint32_t i = min(q / ST::PPR, kPfRows - 1);
+        const RowPos rp = row_pos(W, min(r0 + i, W.rows - 1));
+        pc[j] = Piece{rp.tile, rp.lanes, rp.ln0, q < PIECES ? q : PIECES};
+    }
+    struct Staged {
+        uint4 v[PPT];
+    };
+    auto load_pieces = [&](uint32_t ph) {
+        Staged R;
+#pragma unroll
+        for (uint32_t j = 0; j < PPT; j++) {
+            const Piece &P = pc[j];
+            const uint32_t q = min(P.q, PIECES - 1), r = q % ST::PPR;
+            uint64_t off;
+            if constexpr (T == PI_TYPE_Q4_K) {
+                const uint32_t c = r >> 1, v = r & 1u, u = min(ph * ST::PB + v, nb - 1);
+                off = (uint64_t)((1u + c) * P.lanes + P.ln0 + u) * 16u;
+            } else if constexpr (T == PI_TYPE_Q6_K) {
+                off = (uint64_t)(r * P.lanes + P.ln0 + min(ph, nb - 1)) * 16u;
+            } else {
+                constexpr uint32_t BC = T == PI_TYPE_Q8_0 ? 2u : 1u;
+                const uint32_t v = r / BC, jc = r - v * BC, u = min(ph * ST::PB + v, nb - 1);
+                const uint32_t unit = div_g(W, u), b = u - unit * W.g;
+                off = (uint64_t)((b * BC + jc) * P.lanes + P.ln0 + unit) * 16u;
+            }
+            R.v[j] = *gld(reinterpret_cast<const uint4 *>(P.tile + off));
+        }
+        return R;
+    };
+    auto store_pieces = [&](const Staged &R, uint4 *wb) {
+#pragma unroll
+        for (uint32_t j = 0; j < PPT; j++)
+            if (pc[j].q < PIECES) wb[(pc[j].q / ST::PPR) * ST::WS + pc[j].q % ST::PPR] = R.v[j];
+    };
+
+    // ---- activation operands -----------------------------------------------
+    const uint32_t n = th * 16 + li;   // this lane's MFMA token
+    auto act_group = [&](uint32_t tg) -> uint32_t {
+        if constexpr (T == PI_TYPE_Q6_K) return (tg >> 4) * 8 + 4 * ((tg >> 3) & 1u) + (tg & 3u);
+        else return tg;
+    };
+    struct PhaseAct {
+        TermAct A[kPfTermsPerWave];
+    };
+    auto load_act = [&](uint32_t ph) {
+        PhaseAct P;
+#pragma unroll
+        for (uint32_t j = 0; j < kPfTermsPerWave; j++) {
+            const uint32_t a = act_group(min(ph * kPfPhase + w * kPfTermsPerWave + j, tpr - 1));
+            P.A[j].b = *gld(reinterpret_cast<const uint2 *>(aq + pfq_off(a, ka, n)));
+            P.A[j].da = *gld(ad + a * PI_PF_MAX_TOK + n);
+            if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q4_0) P.A[j].as = *gld(as + a * PI_PF_MAX_TOK + n);
+        }
+        return P;
+    };
+
+    // the 4 terms of rows 4*ka..4*ka+3 for this lane's token
+    auto term4 = [&](const TermAct &X, const uint4 *wb, uint32_t ph, uint32_t tg, float (&t)[4]) {
+        const long B = pack2(X.b.x, X.b.y);
+        const uint8_t *wrow = reinterpret_cast<const uint8_t *>(wb + li * ST::WS) + 8u * (ka & 1u);
+        if constexpr (T == PI_TYPE_Q4_K) {
+            const uint32_t u = tg >> 3, sb = tg & 7u, v = u - ph * ST::PB;
+            const uint2 a = *reinterpret_cast<const uint2 *>(wrow + ((2u * (sb >> 1) + (ka >> 1)) * 2u + v) * 16u);
+            const uint32_t sh = (sb & 1u) * 4u;
+            const v4i cc = mfma16(pack2((a.x >> sh) & 0x0F0F0F0Fu, (a.y >> sh) & 0x0F0F0F0Fu), B);
+            const float *c = cst + (uint64_t)u * PfLds<T>::floats_per_block;
+            const float4 d4 = reinterpret_cast<const float4 *>(c)[ka];
+            const float4 dm4 = reinterpret_cast<const float4 *>(c + 16)[ka];
+            const float4 s4 = reinterpret_cast<const float4 *>(c + 32 + sb * 16)[ka];
+            const float4 m4 = reinterpret_cast<const float4 *>(c + 160 + sb * 16)[ka];
+            const float asf = (float)X.as;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                t[i] = f4(d4, i) * X.da * f4(s4, i) * (float)cc[i] - X.da * f4(dm4, i) * f4(m4, i) * asf;
+        } else if constexpr (T == PI_TYPE_Q6_K) {
+            const uint32_t u = tg >> 4, half = (tg >> 3) & 1u, g = (tg >> 2) & 1u, s = tg & 3u;
+            const uint2 ql = *reinterpret_cast<const uint2 *>(wrow + (half * 4 + 2 * (s & 1u) + (ka >> 1)) * 16u);
+            const uint2 qh = *reinterpret_cast<const uint2 *>(wrow + (8 + half * 2 + (ka >> 1)) * 16u);
+            const bool mine = (ka >> 1) == g;   // this lane's 8 elements are in 16-group g
+            uint32_t w6[2];
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t l4 = e ? ql.y : ql.x, h2 = e ? qh.y : qh.x;
+                const uint32_t nib = s < 2 ? (l4 & 0x0F0F0F0Fu) : ((l4 >> 4) & 0x0F0F0F0Fu);
+                const uint32_t q = nib | (((h2 >> (2 * s)) & 0x03030303u) << 4);   // 0..63 per byte
+                const uint32_t x = q ^ 0x20202020u;                               // q - 32 in 6 bits
+                w6[e] = x | ((x & 0x20202020u) * 6u);                              // sign-extend to 8
+            }
+            const v4i cc = mfma16(mine ? pack2(w6[0], w6[1]) : 0L, B);
+            const float4 ds4 =
+                reinterpret_cast<const float4 *>(cst + (uint64_t)u * PfLds<T>::floats_per_block + (half * 8 + g + 2 * s) * 16)[ka];
+#pragma unroll
+            for (int i = 0; i < 4; i++) t[i] = f4(ds4, i) * X.da * (float)cc[i];
+        } else {
+            const uint32_t v = tg - ph * ST::PB;
+            long A;
+            if constexpr (T == PI_TYPE_Q8_0) {
+                const uint2 a = *reinterpret_cast<const uint2 *>(wrow + (v * 2u + (ka >> 1)) * 16u);
+                A = pack2(a.x, a.y);
+            } else {
+                const uint2 a = *reinterpret_cast<const uint2 *>(wrow + v * 16u);
+                const uint32_t sh = (ka >> 1) * 4u;
+                A = pack2((a.x >> sh) & 0x0F0F0F0Fu, (a.y >> sh) & 0x0F0F0F0Fu);
+            }
+            const v4i cc = mfma16(A, B);
+            const float4 d4 = reinterpret_cast<const float4 *>(cst + (uint64_t)tg * PfLds<T>::floats_per_block)[ka];
+            if constexpr (T == PI_TYPE_Q8_0) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) t[i] = f4(d4, i) * X.da * (float)cc[i];
+            } else {
+                const float asf = (float)X.as;
+#pragma unroll
+                for (int i = 0; i < 4; i++) t[i] = f4(d4, i) * X.da * ((float)cc[i] - 8.0f * asf);
+            }
+        }
+    };
+
+    // ---- phases ---------------------------------------------------------------
+    float acc = 0.0f;
+    // pair of this thread: token pn, row pr.  Plane address row * 20 + token:
+    // the 64 lanes of a wavefront (4 tokens x 16 rows) and of each term
+    // write (16 tokens x rows 4*ka + i) fall on 64 distinct banks.
+    const uint32_t pn = tid >> 4, pr = tid & 15u;
+    Staged SW = load_pieces(0);
+    PhaseAct TA = load_act(0);
+    decode_consts<T>(W, r0, nb, cst);
+    store_pieces(SW, wb0);
+    SW = load_pieces(min(1u, nph - 1));
+    __syncthreads();
+    for (uint32_t ph = 0; ph < nph; ph++) {
+        const PhaseAct TN = load_act(min(ph + 1, nph - 1));
+        const uint4 *wb = (ph & 1u) ? wb1 : wb0;
+        float *pl = (ph & 1u) ? pl1 : pl0;
+#pragma unroll
+        for (uint32_t j = 0; j < kPfTermsPerWave; j++) {
+            const uint32_t jj = w * kPfTermsPerWave + j, tg = ph * kPfPhase + jj;
+            if (tg < tpr) {
+                float t[4];
+                term4(TA.A[j], wb, ph, tg, t);
+#pragma unroll
+                for (int i = 0; i < 4; i++) pl[jj * kPfPlane + (4 * ka + i) * kPfTokPad + li] = t[i];
+            }
+        }
+        if (ph + 1 < nph) store_pieces(SW, (ph & 1u) ? wb0 : wb1);
+        SW = load_pieces(min(ph + 2, nph - 1));
+        __syncthreads();
+        const float *col = pl + pr * kPfTokPad + pn;
+        const uint32_t lim = min(kPfPhase, tpr - ph * kPfPhase);
+        if (lim == kPfPhase) {
+            float v[kPfPhase];
+#pragma unroll
+            for (uint32_t q = 0; q < kPfPhase; q++) v[q] = col[q * kPfPlane];
+#pragma unroll
+            for (uint32_t q = 0; q < kPfPhase; q++) acc += v[q];
+        } else {
+            for (uint32_t q = 0; q < lim; q++) acc += col[q * kPfPlane];
+        }
+        TA = TN;
+    }
+    const uint32_t tok = th * 16 + pn, r = r0 + pr;
+    if (tok < ntok && r < W.rows) {
+        float *o = out + (uint64_t)tok * W.rows + r;
+        const float v = 0.0f + acc;
+        *o = resid ? *o + v : v;
     }
 }
 
@@ -234,57 +454,88 @@ __global__ __launch_bounds__(256) void k_pf_embed(const uint8_t *__restrict__ E,
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm (scalar order) + Q8 of one token per workgroup.
+// RMSNorm (scalar order) + Q8 of one token per workgroup.  The row and its
+// squares are staged in LDS (the squares padded by floats the chain reads
+// ahead); thread 0 adds the squares in order; pairs of lanes then quantize
+// half a block each.
 // ---------------------------------------------------------------------------
+constexpr uint32_t kNormPad = 32;
+
 __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X, const float *__restrict__ w,
-                                                    uint32_t ne, float eps, int8_t *__restrict__ q,
-                                                    float *__restrict__ d, int32_t *__restrict__ s) {
+                                                    uint32_t ne, float eps, pi_pf_q8 o) {
     extern __shared__ __align__(16) float xs[];
     __shared__ float sv;
     const uint32_t t = blockIdx.x, tid = threadIdx.x, nb = ne / 32;
+    float *sq = xs + ne + kNormPad;   // squares, rounded as the loop rounds them
     const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * ne);
-    for (uint32_t i = tid; i < ne / 4; i += blockDim.x) reinterpret_cast<float4 *>(xs)[i] = x4[i];
+    for (uint32_t i = tid; i < ne / 4; i += blockDim.x) {
+        const float4 v = x4[i];
+        reinterpret_cast<float4 *>(xs)[i] = v;
+        reinterpret_cast<float4 *>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    }
+    if (tid < kNormPad) sq[ne + tid] = 0.0f;
     __syncthreads();
     if (tid == 0) {
+        // ss += v * v in order (model.rs:812-822): the products are formed above
         float ss = 0.0f;
-        lds_fold4<6>(reinterpret_cast<const float4 *>(xs), ne / 4, [&](const float4 &v) {
-            ss += v.x * v.x;
-            ss += v.y * v.y;
-            ss += v.z * v.z;
-            ss += v.w * v.w;
+        lds_chain4<8>(reinterpret_cast<const float4 *>(sq), ne / 4, [&](const float4 &q) {
+            ss += q.x;
+            ss += q.y;
+            ss += q.z;
+            ss += q.w;
         });
         sv = 1.0f / sqrtf(ss / (float)ne + eps);
     }
     __syncthreads();
     const float sc = sv;
-    for (uint32_t b = tid; b < nb; b += blockDim.x) {
-        float v[32];
+    for (uint32_t p = tid; p < 2 * nb; p += blockDim.x) {   // pairs of lanes stay together
+        const uint32_t b = p >> 1, hh = p & 1u;
+        const float4 *xv = reinterpret_cast<const float4 *>(xs + 16 * p);
+        const float4 *wv = reinterpret_cast<const float4 *>(w + 16 * p);
+        float v[16];
 #pragma unroll
-        for (int j = 0; j < 32; j++) v[j] = xs[32 * b + j] * sc * w[32 * b + j];
-        q8_lane(v, reinterpret_cast<uint32_t *>(q + (uint64_t)t * ne) + 8 * b, d + (uint64_t)t * nb + b,
-                s + (uint64_t)t * nb + b);
+        for (int j = 0; j < 4; j++) {
+            const float4 xx = xv[j], ww = wv[j];
+            v[4 * j + 0] = xx.x * sc * ww.x;
+            v[4 * j + 1] = xx.y * sc * ww.y;
+            v[4 * j + 2] = xx.z * sc * ww.z;
+            v[4 * j + 3] = xx.w * sc * ww.w;
+        }
+        uint32_t w4[4];
+        float dd;
+        int sum;
+        q8_pair_core(v, w4, dd, sum);
+        pf_store_pair(o, t, b, hh, w4, dd, sum);
     }
 }
 
 // ---------------------------------------------------------------------------
-// h = silu(gate) * up, then Q8 of h (one token per workgroup).
+// h = silu(gate) * up, then Q8 of h: a lane per half block, a pair per block.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ G, const float *__restrict__ U,
-                                                      uint32_t n_ff, int8_t *__restrict__ q, float *__restrict__ d,
-                                                      int32_t *__restrict__ s) {
+                                                      uint32_t n_ff, pi_pf_q8 o) {
     const uint32_t t = blockIdx.x, nb = n_ff / 32;
-    for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
-        float v[32];
-        const float *g = G + (uint64_t)t * n_ff + 32 * b, *u = U + (uint64_t)t * n_ff + 32 * b;
+    const uint32_t p = blockIdx.y * blockDim.x + threadIdx.x;
+    if (p >= 2 * nb) return;   // 2 * nb is even: pairs stay together
+    const uint32_t b = p >> 1, hh = p & 1u;
+    const float4 *g4 = reinterpret_cast<const float4 *>(G + (uint64_t)t * n_ff + 16 * p);
+    const float4 *u4 = reinterpret_cast<const float4 *>(U + (uint64_t)t * n_ff + 16 * p);
+    float v[16];
 #pragma unroll
-        for (int j = 0; j < 32; j++) {
-            const float gg = g[j];
-            const float sg = gg / (1.0f + pi_expf(-gg));
-            v[j] = sg * u[j];
+    for (int j = 0; j < 4; j++) {
+        const float4 gg = g4[j], uu = u4[j];
+        const float ga[4] = {gg.x, gg.y, gg.z, gg.w}, ua[4] = {uu.x, uu.y, uu.z, uu.w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float sg = ga[e] / (1.0f + pi_expf(-ga[e]));
+            v[4 * j + e] = sg * ua[e];
         }
-        q8_lane(v, reinterpret_cast<uint32_t *>(q + (uint64_t)t * n_ff) + 8 * b, d + (uint64_t)t * nb + b,
-                s + (uint64_t)t * nb + b);
     }
+    uint32_t w4[4];
+    float dd;
+    int sum;
+    q8_pair_core(v, w4, dd, sum);
+    pf_store_pair(o, t, b, hh, w4, dd, sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -329,87 +580,215 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(float *__restrict__ Q, const
 }
 
 // ---------------------------------------------------------------------------
-// Attention: a workgroup serves 4 tokens (one per wavefront) of one head and
-// stages 64 K, then V rows at a time through LDS for all four.
-// Scores: lane = position, scalar dot in d order, * scale.  Values: lane =
-// dimension, in position order: sum += e_p; acc += e_p * v_p[d] unless
-// e_p == 0.  Output acc * (1/sum), then Q8 of the head's 64 values.
+// Attention: a workgroup serves 4 tokens of one head with 5 wavefronts.  K,
+// then V, rows are staged through two LDS buffers 64 positions per step by
+// wavefronts 0-3, each step's rows loaded into registers two steps ahead
+// (one barrier per step).
+// Scores (model.rs:1028-1038, scalar dot in d order, * scale): wavefront t
+// serves token t, lane = position.  Then e_p = exp(s_p - max) lane-parallel,
+// and a flag per step if any e_p is 0.  Values (f32_axpy order, products
+// rounded, e_p == 0 skipped): wavefront t adds e_p * v_p[d] in position
+// order, lane = dimension, from the transposed V step; meanwhile lane t of
+// wavefront 4 adds sum += e_p of token t in position order.
+// Output acc * (1/sum), then Q8 of the head's 64 values.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kKvPad = 65;
+constexpr uint32_t kAttStep = 64;               // positions per staged step
+constexpr uint32_t kAttThreads = 320;
+constexpr uint32_t kKRow = 68;                  // floats per staged K row
+constexpr uint32_t kVRow = kAttStep + 4;        // floats per staged transposed V row
+constexpr uint32_t kAttBuf = kAttStep * kKRow;  // floats per staging buffer (>= 64 * kVRow)
+static_assert(kAttBuf >= 64 * kVRow, "staging buffer holds a transposed V step");
 
-__global__ __launch_bounds__(256) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
-                                                 const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
-                                                 uint32_t n_head, uint32_t group, uint32_t n_ctx, float scale,
-                                                 int8_t *__restrict__ oq, float *__restrict__ od,
-                                                 int32_t *__restrict__ os) {
+__global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
+                                                         const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
+                                                         uint32_t n_head, uint32_t group, uint32_t n_ctx, float scale,
+                                                         int8_t *__restrict__ oq, float *__restrict__ od,
+                                                         int32_t *__restrict__ os) {
     constexpr uint32_t DH = 64;
     extern __shared__ __align__(16) float lds[];
-    float *kv = lds;                          // 64 x 65
-    float *qs = kv + 64 * kKvPad;             // 4 x 64
-    float *sc = qs + 4 * DH;                  // 4 x n_ctx
-    const uint32_t h = blockIdx.x % n_head, tg = blockIdx.x / n_head;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, tid = threadIdx.x;
-    const uint32_t t = 4 * tg + wave;
-    const bool valid = t < ntok;
-    const uint32_t pos_t = pos0 + t;          // positions 0..pos_t (valid tokens)
+    float *const buf0 = lds, *const buf1 = lds + kAttBuf;
+    float *qs = lds + 2 * kAttBuf;              // 4 x 64
+    float *misc = qs + 4 * DH;                  // 16 floats: per-token max and sum
+    uint32_t *zflag = reinterpret_cast<uint32_t *>(misc + 16);   // [4][nsteps]
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch): every workgroup of
+    // head h gets b % 8 == h % 8, so a head's K/V rows are read into one L2.
+    const uint32_t ntg = (ntok + 3) / 4, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
+    const uint32_t tg = rest % ntg, h = (rest / ntg) * 8 + xcd;
+    if (h >= n_head) return;   // before any barrier: the whole workgroup leaves
+    const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+    const bool stager = w < 4;
+    const uint32_t tok = w & 3u;
+    const uint32_t t = 4 * tg + tok;
+    const bool valid = w < 4 && t < ntok;
+    const uint32_t pos_t = pos0 + t;
     const uint32_t n_all = pos0 + min(4 * tg + 3, ntok - 1) + 1;
+    const uint32_t nsteps = (n_all + kAttStep - 1) / kAttStep;
+    const uint32_t scs = (n_ctx + 3) & ~3u;    // row stride of the scores
+    float *sc = reinterpret_cast<float *>(zflag + 4 * ((nsteps + 3) & ~3u));   // [4][scs] scores, then e
+    float *sct = sc + (uint64_t)tok * scs;
     const uint32_t kvh = h / group, qdim = n_head * DH;
     const float *kbase = kc + (uint64_t)kvh * n_ctx * DH, *vbase = vc + (uint64_t)kvh * n_ctx * DH;
-    float *scw = sc + (uint64_t)wave * n_ctx;
-    qs[wave * DH + lane] = valid ? Q[(uint64_t)t * qdim + h * DH + lane] : 0.0f;
-    float mx = -INFINITY;
-    auto stage = [&](const float *base, uint32_t c0, uint32_t rows) {
-        for (uint32_t i = tid; i < rows * 16; i += 256) {
-            const uint32_t p = i / 16, f = i % 16;
-            const float4 v = reinterpret_cast<const float4 *>(base + (uint64_t)(c0 + p) * DH)[f];
-            float *dst = kv + p * kKvPad + 4 * f;
-            dst[0] = v.x;
-            dst[1] = v.y;
-            dst[2] = v.z;
-            dst[3] = v.w;
+
+    if (w < 4) qs[tok * DH + lane] = t < ntok ? Q[(uint64_t)t * qdim + h * DH + lane] : 0.0f;
+    for (uint32_t i = tid; i < 4 * nsteps; i += kAttThreads) zflag[i] = 0u;
+
+    // staging (wavefronts 0-3): row i = tid / 4 of the step, float4 columns 4*(tid%4)..+3
+    const uint32_t srow = tid >> 2, sf = (tid & 3u) * 4u;
+    struct Rows {
+        float4 v[4];
+    };
+    // rows of wavefronts 4+ are a clamped in-bounds copy of row 0 (never stored)
+    auto load_rows = [&](const float *base, uint32_t c) -> Rows {
+        const uint32_t p = stager ? min(c * kAttStep + srow, n_all - 1) : 0u;
+        const float4 *src = reinterpret_cast<const float4 *>(base + (uint64_t)p * DH) + (stager ? sf : 0u);
+        Rows R;
+#pragma unroll
+        for (int j = 0; j < 4; j++) R.v[j] = src[j];
+        return R;
+    };
+    auto store_k = [&](const Rows R, float *bf) {
+        if (!stager) return;
+#pragma unroll
+        for (int j = 0; j < 4; j++) reinterpret_cast<float4 *>(bf + srow * kKRow)[sf + j] = R.v[j];
+    };
+    auto store_vt = [&](const Rows R, float *bf) {
+        if (!stager) return;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t d = 4 * (sf + j);
+            bf[(d + 0) * kVRow + srow] = R.v[j].x;
+            bf[(d + 1) * kVRow + srow] = R.v[j].y;
+            bf[(d + 2) * kVRow + srow] = R.v[j].z;
+            bf[(d + 3) * kVRow + srow] = R.v[j].w;
         }
     };
-    for (uint32_t c0 = 0; c0 < n_all; c0 += 64) {
-        const uint32_t rows = min(64u, n_all - c0);
+    // Runs body(c, buffer of step c) for every step; rows of step c + 1 are
+    // stored while step c is used, rows of step c + 2 are in flight.
+    auto stream = [&](const float *base, auto transposed, auto &&body) {
+        auto put = [&](const Rows R, float *bf) {
+            if constexpr (decltype(transposed)::value) store_vt(R, bf);
+            else store_k(R, bf);
+        };
+        Rows A = load_rows(base, 0);
+        Rows B = load_rows(base, min(1u, nsteps - 1));
+        put(A, buf0);
         __syncthreads();
-        stage(kbase, c0, rows);
-        __syncthreads();
-        const uint32_t p = c0 + lane;
-        if (valid && lane < rows && p <= pos_t) {
+        A = load_rows(base, min(2u, nsteps - 1));
+        for (uint32_t c = 0; c < nsteps; c += 2) {
+            body(c, buf0);
+            if (c + 1 < nsteps) put(B, buf1);
+            __syncthreads();
+            if (c + 1 >= nsteps) break;
+            B = load_rows(base, min(c + 3, nsteps - 1));
+            body(c + 1, buf1);
+            if (c + 2 < nsteps) put(A, buf0);
+            __syncthreads();
+            A = load_rows(base, min(c + 4, nsteps - 1));
+        }
+    };
+
+    // ---- pass 1: scores and maximum -------------------------------------
+    float mx = -INFINITY;
+    stream(kbase, std::false_type{}, [&](uint32_t c, const float *cur) {
+        const uint32_t p = c * kAttStep + lane;
+        if (valid && p <= pos_t) {
+            const float4 *kr = reinterpret_cast<const float4 *>(cur + lane * kKRow);
+            const float4 *q4 = reinterpret_cast<const float4 *>(qs + tok * DH);
             float s = 0.0f;
-            const float *kr = kv + lane * kKvPad, *qv = qs + wave * DH;
-#pragma unroll 16
-            for (uint32_t dd = 0; dd < DH; dd++) s += qv[dd] * kr[dd];
+#pragma unroll
+            for (int d4 = 0; d4 < 16; d4++) {
+                const float4 kk = kr[d4], qq = q4[d4];
+                s += qq.x * kk.x;
+                s += qq.y * kk.y;
+                s += qq.z * kk.z;
+                s += qq.w * kk.w;
+            }
             s = s * scale;
-            scw[p] = s;
+            sct[p] = s;
             mx = fmaxf(mx, s);
         }
-    }
+    });
 #pragma unroll
     for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (valid)
-        for (uint32_t p = lane; p <= pos_t; p += 64) scw[p] = pi_expf(scw[p] - mx);
+
+    // ---- e_p = exp(s_p - max), zero flags per step -------------------------
+    if (valid) {
+        for (uint32_t c = 0; c < nsteps; c++) {
+            const uint32_t p = c * kAttStep + lane;
+            bool zero = false;
+            if (p <= pos_t) {
+                const float e = pi_expf(sct[p] - mx);
+                sct[p] = e;
+                zero = e == 0.0f;
+            }
+            if (__ballot(zero) && lane == 0) zflag[tok * nsteps + c] = 1u;
+        }
+    }
+    __syncthreads();
+
+    // ---- pass 2: sums in position order ------------------------------------
     float acc = 0.0f, sum = 0.0f;
-    for (uint32_t c0 = 0; c0 < n_all; c0 += 64) {
-        const uint32_t rows = min(64u, n_all - c0);
-        __syncthreads();
-        stage(vbase, c0, rows);
-        __syncthreads();
-        if (valid && pos_t >= c0) {
-            const uint32_t lim = min(rows, pos_t + 1 - c0);
-            for (uint32_t r = 0; r < lim; r++) {
-                const float e = scw[c0 + r];
-                sum += e;
-                const float v = kv[r * kKvPad + lane];
-                acc = (e != 0.0f) ? acc + e * v : acc;
+    const uint32_t stok = lane & 3u, st_t = 4 * tg + stok;   // wavefront 4: lane = token
+    stream(vbase, std::true_type{}, [&](uint32_t c, const float *cur) {
+        const uint32_t p0 = c * kAttStep;
+        if (w < 4) {
+            if (!valid || pos_t < p0) return;
+            const uint32_t lim = min(kAttStep, pos_t + 1 - p0);
+            const float *e = sct + p0, *vr = cur + lane * kVRow;
+            uint32_t r = 0;
+            auto four = [&](uint32_t q) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(e + q);
+                const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
+                acc = acc + e4.x * v4.x;
+                acc = acc + e4.y * v4.y;
+                acc = acc + e4.z * v4.z;
+                acc = acc + e4.w * v4.w;
+            };
+            if (zflag[tok * nsteps + c] == 0u) {
+                if (lim == kAttStep) {
+#pragma unroll
+                    for (uint32_t q = 0; q < kAttStep; q += 4) four(q);
+                    r = kAttStep;
+                } else {
+                    for (; r + 4 <= lim; r += 4) four(r);
+                }
+            }
+            for (; r < lim; r++) {
+                const float ee = e[r];
+                acc = acc + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
+            }
+        } else if (lane < 4 && st_t < ntok && pos0 + st_t >= p0) {
+            const uint32_t lim = min(kAttStep, pos0 + st_t + 1 - p0);
+            const float *e = sc + (uint64_t)stok * scs + p0;
+            uint32_t r = 0;
+            for (; r + 4 <= lim; r += 4) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(e + r);
+                sum += e4.x;
+                sum += e4.y;
+                sum += e4.z;
+                sum += e4.w;
+            }
+            for (; r < lim; r++) sum += e[r];
+        }
+    });
+    if (w == 4 && lane < 4) misc[lane] = sum;
+    __syncthreads();
+    if (w < 4) {
+        const float tot = misc[tok];
+        const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+        const float o = acc * inv;
+        const uint32_t blk = h * 2 + lane / 32, j = lane % 32;
+        float dd;
+        int sum;
+        const int iv = q8_block32_core(o, dd, sum);
+        if (valid) {
+            oq[pfq_off(blk, j / 8, t) + j % 8] = (int8_t)iv;
+            if (j == 0) {
+                od[blk * PI_PF_MAX_TOK + t] = dd;
+                os[blk * PI_PF_MAX_TOK + t] = sum;
             }
         }
     }
-    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-    const float o = acc * inv;
-    const uint32_t nb = qdim / 32, blk = h * 2 + lane / 32;
-    q8_block32(o, (int)(lane % 32), oq + (uint64_t)t * qdim + blk * 32, od + (uint64_t)t * nb + blk,
-               os + (uint64_t)t * nb + blk, valid);
 }
 
 WV to_wv(const pi_pf_mat &M) {
@@ -420,6 +799,7 @@ WV to_wv(const pi_pf_mat &M) {
     W.rpw = M.L.rpw;
     W.lpt = M.L.lpt;
     W.g = M.L.g;
+    W.gmag = M.L.g > 1 ? (uint32_t)((((uint64_t)1 << 32) + M.L.g - 1) / M.L.g) : 0u;
     W.qc = M.L.qc;
     W.ntiles = M.L.ntiles;
     W.tile_bytes = M.L.tile_bytes;
@@ -437,36 +817,63 @@ hipError_t pi_pf_embed(const uint8_t *embd, uint32_t etype, uint64_t row_bytes, 
 
 hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps, uint32_t ntok, pi_pf_q8 o,
                          hipStream_t s) {
-    if (ntok == 0 || ntok > PI_PF_MAX_TOK || ne % 32 || ne / 32 > 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_norm_q8, dim3(ntok), dim3(256), ne * 4, s, X, w, ne, eps, o.q, o.d, o.s);
+    if (ntok == 0 || ntok > PI_PF_MAX_TOK || ne % 32 || ne > 16384) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_pf_norm_q8, dim3(ntok), dim3(256), (2 * ne + 2 * kNormPad) * 4, s, X, w, ne, eps, o);
     return hipGetLastError();
 }
 
-hipError_t pi_pf_gemm(const pi_pf_mat &M, pi_pf_q8 a, uint32_t ntok, float *out, bool resid, hipStream_t s) {
-    if (ntok == 0 || ntok > PI_PF_MAX_TOK || M.L.rows == 0) return hipErrorInvalidValue;
-    const WV W = to_wv(M);
-    const uint32_t waves = (M.L.rows + 15) / 16 * 2, blocks = (waves + 3) / 4;
-    switch (M.L.type) {
-    case PI_TYPE_Q4_K:
-        hipLaunchKernelGGL(k_pf_gemm<PI_TYPE_Q4_K>, dim3(blocks), dim3(256), 0, s, W, a.q, a.d, a.s, M.L.k, ntok, out,
-                           M.L.rows, (int)resid);
-        break;
-    case PI_TYPE_Q6_K:
-        hipLaunchKernelGGL(k_pf_gemm<PI_TYPE_Q6_K>, dim3(blocks), dim3(256), 0, s, W, a.q, a.d, a.s, M.L.k, ntok, out,
-                           M.L.rows, (int)resid);
-        break;
-    case PI_TYPE_Q8_0:
-        hipLaunchKernelGGL(k_pf_gemm<PI_TYPE_Q8_0>, dim3(blocks), dim3(256), 0, s, W, a.q, a.d, a.s, M.L.k, ntok, out,
-                           M.L.rows, (int)resid);
-        break;
-    case PI_TYPE_Q4_0:
-        hipLaunchKernelGGL(k_pf_gemm<PI_TYPE_Q4_0>, dim3(blocks), dim3(256), 0, s, W, a.q, a.d, a.s, M.L.k, ntok, out,
-                           M.L.rows, (int)resid);
-        break;
-    default:
-        return hipErrorInvalidValue;
+hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg, pi_pf_q8 a, uint32_t ntok,
+                             bool resid, hipStream_t s) {
+    if (ntok == 0 || ntok > PI_PF_MAX_TOK || nseg == 0 || nseg > kPfMaxSeg) return hipErrorInvalidValue;
+    const uint32_t t = M[0].L.type, k = M[0].L.k;
+    PfSegs S{};
+    uint32_t wgs = 0;
+    for (uint32_t i = 0; i < nseg; i++) {
+        if (M[i].L.type != t || M[i].L.k != k || M[i].L.rows == 0) return hipErrorInvalidValue;
+        S.W[i] = to_wv(M[i]);
+        S.out[i] = out[i];
+        wgs += (M[i].L.rows + kPfRows - 1) / kPfRows * ((ntok + 15) / 16);
+        S.wg_end[i] = wgs;
     }
-    return hipGetLastError();
+    S.nseg = nseg;
+    const uint32_t nb = k / pi_base_elems(t);
+    size_t cfl = 0;
+    switch (t) {
+    case PI_TYPE_Q4_K: cfl = (size_t)nb * PfLds<PI_TYPE_Q4_K>::floats_per_block; break;
+    case PI_TYPE_Q6_K: cfl = (size_t)nb * PfLds<PI_TYPE_Q6_K>::floats_per_block; break;
+    case PI_TYPE_Q4_0:
+    case PI_TYPE_Q8_0:
+        cfl = (size_t)nb * PfLds<PI_TYPE_Q8_0>::floats_per_block;
+        static_assert(PfLds<PI_TYPE_Q8_0>::floats_per_block == PfLds<PI_TYPE_Q4_0>::floats_per_block, "");
+        break;
+    default: return hipErrorInvalidValue;
+    }
+    uint32_t ws = 0;
+    switch (t) {
+    case PI_TYPE_Q4_K: ws = PfStage<PI_TYPE_Q4_K>::WS; break;
+    case PI_TYPE_Q6_K: ws = PfStage<PI_TYPE_Q6_K>::WS; break;
+    case PI_TYPE_Q8_0: ws = PfStage<PI_TYPE_Q8_0>::WS; break;
+    default: ws = PfStage<PI_TYPE_Q4_0>::WS; break;
+    }
+    const size_t lds = (((cfl + 3) & ~(size_t)3) + 2 * (size_t)kPfPhase * kPfPlane) * 4 + 2 * (size_t)kPfRows * ws * 16;
+    if (lds > 80 * 1024 || nb > 65535) return hipErrorInvalidValue;   // two workgroups per CU
+    const dim3 grid(wgs), block(kPfThreads);
+    auto launch = [&](auto kern) {
+        hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, block, lds, s, S, a.q, a.d, a.s, k, ntok, (int)resid);
+        return hipGetLastError();
+    };
+    switch (t) {
+    case PI_TYPE_Q4_K: return launch(k_pf_gemm<PI_TYPE_Q4_K>);
+    case PI_TYPE_Q6_K: return launch(k_pf_gemm<PI_TYPE_Q6_K>);
+    case PI_TYPE_Q8_0: return launch(k_pf_gemm<PI_TYPE_Q8_0>);
+    default: return launch(k_pf_gemm<PI_TYPE_Q4_0>);
+    }
+}
+
+hipError_t pi_pf_gemm(const pi_pf_mat &M, pi_pf_q8 a, uint32_t ntok, float *out, bool resid, hipStream_t s) {
+    return pi_pf_gemm_multi(&M, &out, 1, a, ntok, resid, s);
 }
 
 hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *cos_tab, const float *sin_tab,
@@ -478,7 +885,10 @@ hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *
     return hipGetLastError();
 }
 
-size_t pi_pf_attn_lds_bytes(uint32_t n_ctx) { return (size_t)(64 * kKvPad + 4 * 64 + 4 * (size_t)n_ctx) * 4; }
+size_t pi_pf_attn_lds_bytes(uint32_t n_ctx) {
+    const size_t nsteps = (n_ctx + kAttStep - 1) / kAttStep;
+    return (2 * (size_t)kAttBuf + 4 * 64 + 16 + 4 * ((nsteps + 3) & ~(size_t)3) + 4 * (((size_t)n_ctx + 3) & ~(size_t)3)) * 4;
+}
 
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
                       uint32_t n_kv, uint32_t n_ctx, float scale, pi_pf_q8 o, hipStream_t s) {
@@ -486,14 +896,14 @@ hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t
     const size_t lds = pi_pf_attn_lds_bytes(n_ctx);
     hipError_t e = hipFuncSetAttribute((const void *)k_pf_attn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    const uint32_t blocks = n_head * ((ntok + 3) / 4);
-    hipLaunchKernelGGL(k_pf_attn, dim3(blocks), dim3(256), lds, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv, n_ctx,
-                       scale, o.q, o.d, o.s);
+    const uint32_t blocks = 8 * ((ntok + 3) / 4) * ((n_head + 7) / 8);
+    hipLaunchKernelGGL(k_pf_attn, dim3(blocks), dim3(kAttThreads), lds, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
+                       n_ctx, scale, o.q, o.d, o.s);
     return hipGetLastError();
 }
 
 hipError_t pi_pf_swiglu_q8(const float *G, const float *U, uint32_t ntok, uint32_t n_ff, pi_pf_q8 o, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || n_ff % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_swiglu_q8, dim3(ntok), dim3(256), 0, s, G, U, n_ff, o.q, o.d, o.s);
+    hipLaunchKernelGGL(k_pf_swiglu_q8, dim3(ntok, (n_ff / 16 + 255) / 256), dim3(256), 0, s, G, U, n_ff, o);
     return hipGetLastError();
 }
