@@ -296,7 +296,7 @@ template <uint32_t T, int G, int MODE>
 __global__ __launch_bounds__(64) void k_gemv(MatSet S, const int8_t *__restrict__ aq, const float *__restrict__ ad,
                                              const int32_t *__restrict__ as, int32_t *__restrict__ sums) {
     constexpr int TPU = QT<T>::TPB * G;
-    __shared__ __align__(16) float strip[64 * TPU];
+    __shared__ __align__(16) float strip[64 * TPU + kChainPad];
     const uint32_t lane = threadIdx.x & 63u;
     Slice<T, G> SL;
     SL.load(aq, ad, as, lane % S.upr);
@@ -524,7 +524,7 @@ MatSet to_set(const pi_matset &M) {
     return S;
 }
 
-uint32_t strip_bytes(uint32_t tpu) { return (kThreads / 64) * 64 * tpu * 4; }
+uint32_t strip_bytes(uint32_t tpu) { return ((kThreads / 64) * 64 * tpu + kChainPad) * 4; }
 
 template <bool NEON, uint32_t TA, uint32_t TB, int EPI>
 hipError_t launch_norm_gemv(const pi_norm_gemv_args &a, hipStream_t s) {

@@ -525,18 +525,17 @@ __device__ __forceinline__ void lds_fold4(const float4 *p, uint32_t n4, F &&f) {
     for (uint32_t i = nb * B; i < n4; i++) f(p[i]);
 }
 
-// Float4 reads in flight per row sum: deep batches shorten a single
-// wavefront's chain (the persistent kernel, one wavefront per SIMD); the
-// standalone GEMVs keep registers low so more wavefronts share a SIMD.
-#ifndef PI_CHAIN_BATCH
-#define PI_CHAIN_BATCH 1
-#endif
+// Floats readable after the end of every row a chain_sum reads (strips are
+// followed by this much LDS).
+constexpr uint32_t kChainPad = 32;
 
 // Sums n terms of the strip at p strictly left to right, starting from 0.
+// The next 6 float4 are read while the current ones are added (p[n .. n+24)
+// is read ahead and ignored).
 __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
     float acc = 0.0f;
     if ((n & 3u) == 0) {
-        lds_fold4<PI_CHAIN_BATCH>(reinterpret_cast<const float4 *>(p), n / 4, [&](const float4 &v) {
+        lds_chain4<6>(reinterpret_cast<const float4 *>(p), n / 4, [&](const float4 &v) {
             acc += v.x;
             acc += v.y;
             acc += v.z;

@@ -30,7 +30,6 @@
 
 #include <type_traits>
 
-#define PI_CHAIN_BATCH 6
 #include "pi_mega.h"
 
 using namespace pig;

@@ -294,7 +294,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
                 const uint32_t c = r >> 1, v = r & 1u, u = min(ph * ST::PB + v, nb - 1);
                 off = (uint64_t)((1u + c) * P.lanes + P.ln0 + u) * 16u;
             } else if constexpr (T == PI_TYPE_Q6_K) {
-                off = (uint64_t)(r * P.lanes + P.ln0 + min(ph, nb - 1)) * 16u;
+                off = (uint64_t)(r * P.lanes + P.ln0 + min(ph * ST::PB, nb - 1)) * 16u;
             } else {
                 constexpr uint32_t BC = T == PI_TYPE_Q8_0 ? 2u : 1u;
                 const uint32_t v = r / BC, jc = r - v * BC, u = min(ph * ST::PB + v, nb - 1);
