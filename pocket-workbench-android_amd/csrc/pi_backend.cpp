@@ -74,6 +74,7 @@ struct Engine {
     uint64_t *mega_part = nullptr;
     int32_t *mega_abort = nullptr;
     uint64_t *mega_trace = nullptr;  // per-workgroup stage timestamps when tracing
+    uint64_t *mega_amax = nullptr, *mega_aexp = nullptr;   // long-context attention words
     uint32_t mega_blocks = 0, epoch = 0;
     size_t mega_lds = 0;
     // batched prefill (pi_prefill.hip): token-major chunk buffers
@@ -261,7 +262,7 @@ void engine_free(Engine *e) {
     }
     free_tensor(e->head);
     for (void *p : {(void *)e->mega_dev, (void *)e->mega_layers, (void *)e->mega_words, (void *)e->mega_part,
-                    (void *)e->mega_abort, (void *)e->mega_trace})
+                    (void *)e->mega_abort, (void *)e->mega_trace, (void *)e->mega_amax, (void *)e->mega_aexp})
         dfree(p);
     for (void *p : {(void *)e->pfX, (void *)e->pfQ, (void *)e->pfK, (void *)e->pfV, (void *)e->pfG, (void *)e->pfU,
                     (void *)e->pfq, (void *)e->pfd, (void *)e->pfs, (void *)e->pf_ids})
@@ -455,7 +456,8 @@ pig::MatSet mset(std::initializer_list<const pi_tensor *> ts) {
 int build_mega(pi_ctx *c, Engine &e) {
     e.mega_ok = false;
     const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
-    if (e.n_embd % 128 || e.n_embd / 16 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64) return PI_OK;
+    if (e.n_embd % 128 || e.n_embd / 16 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64 || e.n_layer > 63)
+        return PI_OK;
     int maxlds = 0;
     if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;
     e.mega_lds = pi_mega_lds_bytes(e.n_embd, e.n_ff, e.n_ctx);
@@ -465,8 +467,12 @@ int build_mega(pi_ctx *c, Engine &e) {
     const uint64_t per = pi_mega_layer_words(e.n_embd, e.n_ff, qdim, kdim);
     int r;
     if ((r = dalloc(c, &e.mega_words, per * e.n_layer)) || (r = dalloc(c, &e.mega_part, 2ull * e.mega_blocks)) ||
-        (r = dalloc(c, &e.mega_abort, 1)) || (r = dalloc(c, &e.mega_layers, e.n_layer)) || (r = dalloc(c, &e.mega_dev, 1)))
+        (r = dalloc(c, &e.mega_abort, 1)) || (r = dalloc(c, &e.mega_layers, e.n_layer)) || (r = dalloc(c, &e.mega_dev, 1)) ||
+        (r = dalloc(c, &e.mega_amax, (uint64_t)e.n_head * PI_MEGA_MAX_SEG)) ||
+        (r = dalloc(c, &e.mega_aexp, (uint64_t)e.n_head * e.n_ctx)))
         return r;
+    HIPC(c, hipMemset(e.mega_amax, 0, (uint64_t)e.n_head * PI_MEGA_MAX_SEG * 8));
+    HIPC(c, hipMemset(e.mega_aexp, 0, (uint64_t)e.n_head * e.n_ctx * 8));
     HIPC(c, hipMemset(e.mega_words, 0, per * e.n_layer * 8));
     HIPC(c, hipMemset(e.mega_part, 0, 2ull * e.mega_blocks * 8));
     HIPC(c, hipMemset(e.mega_abort, 0, 4));
@@ -521,6 +527,8 @@ int build_mega(pi_ctx *c, Engine &e) {
     a.tok_state = &e.st->tok;
     a.abort_flag = e.mega_abort;
     a.trace = nullptr;
+    a.amax = e.mega_amax;
+    a.aexp = e.mega_aexp;
     HIPC(c, hipMemcpy(e.mega_dev, &a, sizeof a, hipMemcpyHostToDevice));
     e.mega_ok = true;
     return PI_OK;
@@ -603,7 +611,20 @@ hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, u
 // One token through the persistent kernel (layers, and the head when `head`).
 hipError_t mega_token(const pi_ctx *c, Engine &e, int32_t pos, uint32_t tok_imm, const uint32_t *tok_src,
                       uint32_t *id_out, bool neon, bool head) {
-    if (++e.epoch == 0) e.epoch = 1;
+    // Epochs run 1 .. 2^26 - 1 (attention words carry epoch * 64 + layer + 1):
+    // at the wrap every tagged word is cleared, so no stale word can carry the
+    // tag a later launch waits for.
+    if (++e.epoch >= (1u << 26)) {
+        e.epoch = 1;
+        const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
+        hipError_t r;
+        if ((r = hipMemsetAsync(e.mega_words, 0, pi_mega_layer_words(e.n_embd, e.n_ff, qdim, kdim) * e.n_layer * 8,
+                                c->stream)) != hipSuccess ||
+            (r = hipMemsetAsync(e.mega_part, 0, 2ull * e.mega_blocks * 8, c->stream)) != hipSuccess ||
+            (r = hipMemsetAsync(e.mega_amax, 0, (uint64_t)e.n_head * PI_MEGA_MAX_SEG * 8, c->stream)) != hipSuccess ||
+            (r = hipMemsetAsync(e.mega_aexp, 0, (uint64_t)e.n_head * e.n_ctx * 8, c->stream)) != hipSuccess)
+            return r;
+    }
     pi_mega_launch l{tok_src, id_out, tok_imm, pos, e.epoch};
     return pi_launch_mega(e.mega, e.mega_dev, l, neon, head, e.mega_blocks, e.mega_lds, c->stream);
 }

@@ -45,7 +45,14 @@ struct pi_mega_args {
     uint32_t *tok_state;      // receives the greedy id (head launches)
     int32_t *abort_flag;      // set when a wait exceeds its spin bound
     uint64_t *trace;          // optional per-workgroup stage timestamps
+    // Long-context attention (positions split into segments over several
+    // workgroups); words tagged with epoch * 64 + layer + 1, shared by all layers:
+    uint64_t *amax;           // per head, per segment: maximum score (n_head * PI_MEGA_MAX_SEG)
+    uint64_t *aexp;           // per head, per position: e_p (n_head * n_ctx)
 };
+
+constexpr uint32_t PI_MEGA_MAX_SEG = 8;   // segments per head at most
+constexpr uint32_t PI_MEGA_SEG_LEN = 1024;   // positions per segment at least (one segment below)
 
 // What changes from launch to launch.
 struct pi_mega_launch {

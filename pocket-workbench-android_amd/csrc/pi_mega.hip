@@ -136,7 +136,7 @@ struct Cfg {
     const uint8_t *embd;
     uint64_t erow_bytes;
     float *logits;
-    uint64_t *part, *trace;
+    uint64_t *part, *trace, *amax, *aexp;
     uint32_t *tok_state;
     int32_t *abort_flag;
 };
@@ -153,6 +153,7 @@ __device__ __forceinline__ Cfg load_cfg(const pi_mega_args *ap) {
     c.embd = cload(&ap->embd); c.erow_bytes = cload(&ap->erow_bytes);
     c.logits = cload(&ap->logits); c.part = cload(&ap->part); c.trace = cload(&ap->trace);
     c.tok_state = cload(&ap->tok_state); c.abort_flag = cload(&ap->abort_flag);
+    c.amax = cload(&ap->amax); c.aexp = cload(&ap->aexp);
     return c;
 }
 
@@ -476,16 +477,33 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
 // wavefront 0 (lane = dimension) adds the current chunk in order; wavefront
 // 3 also keeps the running sum of e_p.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &L, uint32_t h) {
+__device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &L, uint32_t h,
+                                           uint32_t seg, uint32_t nseg, uint32_t layer) {
     constexpr uint32_t DH = 64;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t group = a.n_head / a.n_kv, kvh = h / group;
     const int pos = r.pos;
     const uint32_t n = (uint32_t)pos + 1;
+    // positions [p0, p1) of this segment; segment 0 also forms the sums
+    const uint32_t p0 = (uint32_t)((uint64_t)seg * n / nseg), p1 = (uint32_t)((uint64_t)(seg + 1) * n / nseg);
+    const uint32_t tag = r.epoch * 64u + layer + 1u;
     const uint64_t *yq = cload(&Yp->q), *yk = cload(&Yp->k), *yv = cload(&Yp->v);
     uint64_t *yatt = cload(&Yp->att);
     float *ykc = cload(&Yp->kc), *yvc = cload(&Yp->vc);
     float *qs = L.red, *kcur = L.red + 64, *vcur = L.red + 128, *misc = L.red + 192;
+    float *kbase = ykc + (uint64_t)kvh * a.n_ctx * DH;
+    float *vbase = yvc + (uint64_t)kvh * a.n_ctx * DH;
+    // Every K row comes from HBM (the row of the current position may not be
+    // visible yet and is recomputed from LDS below), so loads never share a
+    // destination register with an LDS read.
+    auto load_k = [&](uint32_t p, float4 (&kr)[16]) {
+        const PI_GLOBAL float4 *src = gld(reinterpret_cast<const float4 *>(kbase + (uint64_t)p * DH));
+#pragma unroll
+        for (int i = 0; i < 16; i++) kr[i] = src[i];
+    };
+    // the first K row of this thread is requested before the inputs arrive
+    float4 kr[16];
+    if (p0 + tid < p1) load_k(p0 + tid, kr);
     // inputs: q of head h, k and v of its KV head
     bool ok = true;
     if (tid < 3 * DH) {
@@ -508,9 +526,7 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         kcur[2 * i + 1] = y0 * s + y1 * c;
     }
     lds_barrier();
-    float *kbase = ykc + (uint64_t)kvh * a.n_ctx * DH;
-    float *vbase = yvc + (uint64_t)kvh * a.n_ctx * DH;
-    if (h % group == 0 && tid < DH) {
+    if (seg == 0 && h % group == 0 && tid < DH) {
         gst(kbase)[(uint64_t)pos * DH + tid] = kcur[tid];
         gst(vbase)[(uint64_t)pos * DH + tid] = vcur[tid];
     }
@@ -518,14 +534,6 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     // before the current one is used
     float mx = -INFINITY;
     const float4 *q4 = reinterpret_cast<const float4 *>(qs);
-    // Every K row comes from HBM (the row of the current position may not be
-    // visible yet and is recomputed from LDS below), so loads never share a
-    // destination register with an LDS read.
-    auto load_k = [&](uint32_t p, float4 (&kr)[16]) {
-        const PI_GLOBAL float4 *src = gld(reinterpret_cast<const float4 *>(kbase + (uint64_t)p * DH));
-#pragma unroll
-        for (int i = 0; i < 16; i++) kr[i] = src[i];
-    };
     auto score = [&](const float4 (&kr)[16]) {
         float s;
         if (r.neon) {
@@ -553,11 +561,9 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         }
         return s * a.scale;
     };
-    float4 kr[16];
-    if (tid < n) load_k(tid, kr);
-    for (uint32_t p = tid; p < n; p += MT) {
+    for (uint32_t p = p0 + tid; p < p1; p += MT) {
         float4 kn[16];
-        if (p + MT < n) load_k(p + MT, kn);
+        if (p + MT < p1) load_k(p + MT, kn);
         const float s = score(kr);
         if (p != (uint32_t)pos) {
             L.sc[p] = s;
@@ -567,30 +573,6 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         for (int i = 0; i < 16; i++) kr[i] = kn[i];
     }
     vm_drain();
-    if (tid == (uint32_t)pos % MT) {
-        float4 kc4[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) kc4[i] = reinterpret_cast<const float4 *>(kcur)[i];
-        const float s = score(kc4);
-        L.sc[pos] = s;
-        mx = fmaxf(mx, s);
-    }
-#pragma unroll
-    for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-    if (lane == 0) misc[wave] = mx;
-    lds_barrier();
-    mx = fmaxf(fmaxf(misc[0], misc[1]), fmaxf(misc[2], misc[3]));
-    for (uint32_t p = tid; p < n; p += MT) L.sc[p] = pi_expf(L.sc[p] - mx);
-    lds_barrier();
-    trace_detail(a, r, 4);
-
-    // Products e_p * v_p[d] of chunk c go to buffer c & 1, laid out [d][p].
-    // A chunk is 16 groups of 4 positions; wavefronts 1-3 own groups w-1,
-    // w+2, ... (lane l: position 4g + l/16, dimensions 4(l%16)..+3, one
-    // 16-byte load) and keep the V rows of the next kDepth chunks in flight
-    // in registers; wavefront 0 adds chunk c - 1 in order while chunk c is
-    // being formed.  V rows always come from HBM (rows past the end re-read
-    // row n-1); the current position's row is taken from LDS.
     constexpr int GPW = (kChunk / 4 + MW - 2) / (MW - 1);   // groups per product wavefront
     constexpr int kDepth = 4;
     const uint32_t nchunk = (n + kChunk - 1) / kChunk;
@@ -605,6 +587,61 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
             v[i] = gld(reinterpret_cast<const float4 *>(vbase + (uint64_t)p * DH))[lane % 16];
         }
     };
+    // the chain workgroup requests its first V rows before the softmax
+    if (seg == 0 && wave != 0) {
+#pragma unroll
+        for (int k = 0; k < kDepth; k++)
+            if ((uint32_t)k < nchunk) load_v(k, vr[k]);
+    }
+    if (seg == nseg - 1 && tid == ((uint32_t)pos - p0) % MT) {
+        float4 kc4[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) kc4[i] = reinterpret_cast<const float4 *>(kcur)[i];
+        const float s = score(kc4);
+        L.sc[pos] = s;
+        mx = fmaxf(mx, s);
+    }
+#pragma unroll
+    for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) misc[wave] = mx;
+    lds_barrier();
+    mx = fmaxf(fmaxf(misc[0], misc[1]), fmaxf(misc[2], misc[3]));
+    if (nseg > 1) {
+        // maximum over every segment of the head (exact in any order)
+        uint64_t *am = a.amax + (uint64_t)h * PI_MEGA_MAX_SEG;
+        if (tid == 0) ll_put(am + seg, __float_as_uint(mx), tag);
+        bool okm = true;
+        if (tid < nseg) {
+            uint64_t wv = ll_get(am + tid);
+            okm = ll_wait(am + tid, tag, wv, a.abort_flag);
+            misc[8 + tid] = __uint_as_float((uint32_t)wv);
+        }
+        PI_POLL_OR_LEAVE(okm);
+        for (uint32_t i = 0; i < nseg; i++) mx = fmaxf(mx, misc[8 + i]);
+    }
+    for (uint32_t p = p0 + tid; p < p1; p += MT) L.sc[p] = pi_expf(L.sc[p] - mx);
+    if (nseg > 1) {
+        uint64_t *ae = a.aexp + (uint64_t)h * a.n_ctx;
+        if (seg != 0) {
+            for (uint32_t p = p0 + tid; p < p1; p += MT) ll_put(ae + p, __float_as_uint(L.sc[p]), tag);
+            lds_barrier();
+            return true;
+        }
+        // segment 0 adds over every position: e_p of the other segments
+        const bool oke = wg_poll<8>(ae + p1, n - p1, tag, a.abort_flag,
+                                    [&](uint32_t i, uint32_t bits) { L.sc[p1 + i] = __uint_as_float(bits); });
+        PI_POLL_OR_LEAVE(oke);
+    }
+    lds_barrier();
+    trace_detail(a, r, 4);
+
+    // Products e_p * v_p[d] of chunk c go to buffer c & 1, laid out [d][p].
+    // A chunk is 16 groups of 4 positions; wavefronts 1-3 own groups w-1,
+    // w+2, ... (lane l: position 4g + l/16, dimensions 4(l%16)..+3, one
+    // 16-byte load) and keep the V rows of the next kDepth chunks in flight
+    // in registers; wavefront 0 adds chunk c - 1 in order while chunk c is
+    // being formed.  V rows always come from HBM (rows past the end re-read
+    // row n-1); the current position's row is taken from LDS.
     auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
         float *buf = L.hb + (c & 1u) * kChunk * kChunkPad;
 #pragma unroll
@@ -620,11 +657,6 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
             }
         }
     };
-    if (wave != 0) {
-#pragma unroll
-        for (int k = 0; k < kDepth; k++)
-            if ((uint32_t)k < nchunk) load_v(k, vr[k]);
-    }
     float acc = 0.0f, sum = 0.0f;
     for (uint32_t c0 = 0; c0 <= nchunk; c0 += kDepth) {
 #pragma unroll
@@ -991,8 +1023,17 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
         const uint64_t *xin = l == 0 ? nullptr : cload(&a.layers[l - 1].xo);
         if (!stage_qkv(a, r, Y, L, xin, gw, nw)) return;
         trace_mark(a, 2 + 5 * l);
-        for (uint32_t h = nb - 1 - blockIdx.x; h < a.n_head; h += nb)
-            if (!stage_attn(a, r, Y, L, h)) return;
+        {
+            // long contexts split each head's positions into nseg segments, one
+            // workgroup each (at most one item per workgroup: segments wait for
+            // each other)
+            const uint32_t n = (uint32_t)r.pos + 1;
+            uint32_t nseg = (n + PI_MEGA_SEG_LEN - 1) / PI_MEGA_SEG_LEN;
+            nseg = min(nseg, min(PI_MEGA_MAX_SEG, nb / a.n_head));
+            nseg = max(nseg, 1u);
+            for (uint32_t j = nb - 1 - blockIdx.x; j < a.n_head * nseg; j += nb)
+                if (!stage_attn(a, r, Y, L, j % a.n_head, j / a.n_head, nseg, l)) return;
+        }
         trace_mark(a, 3 + 5 * l);
         if (!stage_o(a, r, Y, L, gw, nw)) return;
         trace_mark(a, 4 + 5 * l);
@@ -1026,7 +1067,7 @@ uint32_t pi_mega_blocks(int device, uint32_t ne, uint32_t n_ff, uint32_t n_ctx) 
 
 hipError_t pi_launch_mega(const pi_mega_args &a, const pi_mega_args *a_dev, const pi_mega_launch &l, bool neon,
                           bool head, uint32_t blocks, size_t lds, hipStream_t s) {
-    if (!a_dev || l.epoch == 0 || a.n_layer == 0 || blocks == 0 || a.ne % 32 || a.ne / 32 > MT || a.n_ff / 32 > MT ||
+    if (!a_dev || l.epoch == 0 || l.epoch >= (1u << 26) || a.n_layer == 0 || a.n_layer > 63 || blocks == 0 || a.ne % 32 || a.ne / 32 > MT || a.n_ff / 32 > MT ||
         a.n_ff % 32 || a.half > 32 || a.n_head == 0 || a.n_kv == 0 || a.n_head % a.n_kv || l.pos < 0 ||
         (uint32_t)l.pos >= a.n_ctx || lds < pi_mega_lds_bytes(a.ne, a.n_ff, a.n_ctx))
         return hipErrorInvalidValue;
