@@ -237,7 +237,7 @@ def main():
                    "prompt_tokens": N_PROMPT, "gen_tokens": st["gen_tokens"], "batch": 1},
         "roofline": {"bound": "hbm", "achieved": round(q4k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(q4k_gbs / HBM_PEAK_GBS, 4), "traffic": Q4K_TRAFFIC_BYTES,
-                     "kernel": "Q4_K GEMV 5760x2304 (k_gemv<12,1,0,1>)", "us_per_launch": round(q4k_us, 3),
+                     "kernel": "Q4_K GEMV 5760x2304 (k_gemv<12,1,0>)", "us_per_launch": round(q4k_us, 3),
                      "bytes_per_launch": Q4K_LAUNCH_BYTES},
         "q6k_head_gemv": {"achieved": round(q6k_gbs, 1), "unit": "GB/s", "frac": round(q6k_gbs / HBM_PEAK_GBS, 4),
                           "us_per_launch": round(q6k_us, 3), "bytes_per_launch": Q6K_LAUNCH_BYTES},
