@@ -67,7 +67,7 @@ struct pi_attn_args {
 };
 
 // Standalone GEMV over a matrix set (mode OUT / RESIDUAL / SUMS; SUMS needs
-// n == 1), one wavefront per workgroup, `blocks` persistent workgroups.
+// n == 1): `blocks` persistent wavefronts, four per workgroup.
 hipError_t pi_launch_gemv_set(const pi_matset &M, const int8_t *aq, const float *ad, const int32_t *as,
                               int32_t *sums, int mode, uint32_t blocks, hipStream_t s);
 hipError_t pi_launch_norm_gemv(const pi_norm_gemv_args &a, bool neon, hipStream_t s);

@@ -28,6 +28,7 @@ using namespace pig;
 namespace {
 
 constexpr uint32_t kThreads = 256;  // threads of a fused workgroup (4 wavefronts)
+constexpr uint32_t kGemvThreads = 256;   // standalone GEMV: 4 single-tile wavefronts per workgroup
 
 __host__ __device__ constexpr uint32_t pad32(uint32_t i) { return i + (i >> 5); }
 // floats of the padded staging copy of x, rounded to 16 bytes
@@ -293,21 +294,25 @@ __global__ __launch_bounds__(kThreads) void k_gemv_res(const int8_t *__restrict_
 // workgroup so that small matrices still spread over every CU.
 // ---------------------------------------------------------------------------
 template <uint32_t T, int G, int MODE>
-__global__ __launch_bounds__(64) void k_gemv(MatSet S, const int8_t *__restrict__ aq, const float *__restrict__ ad,
-                                             const int32_t *__restrict__ as, int32_t *__restrict__ sums) {
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(MatSet S, const int8_t *__restrict__ aq,
+                                                       const float *__restrict__ ad, const int32_t *__restrict__ as,
+                                                       int32_t *__restrict__ sums) {
     constexpr int TPU = QT<T>::TPB * G;
-    __shared__ __align__(16) float strip[64 * TPU + kChainPad];
-    const uint32_t lane = threadIdx.x & 63u;
+    constexpr uint32_t W = kGemvThreads / 64;
+    __shared__ __align__(16) float strips[W * 64 * TPU + kChainPad];
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gw = blockIdx.x * W + wave, nw = gridDim.x * W;
+    float *strip = strips + wave * 64 * TPU;
     Slice<T, G> SL;
     SL.load(aq, ad, as, lane % S.upr);
     if constexpr (MODE == PI_GEMV_SUMS) {
-        run_tiles_sums<T, G>(S, SL, blockIdx.x, gridDim.x, sums);
+        run_tiles_sums<T, G>(S, SL, gw, nw, sums);
     } else {
         auto out = [&](uint32_t m, uint32_t row, float v) {
             if constexpr (MODE == PI_GEMV_OUT) S.y[m][row] = v;
             else S.y[m][row] = S.y[m][row] + v;
         };
-        run_tiles<T, G>(S, SL, blockIdx.x, gridDim.x, strip, out);
+        run_tiles<T, G>(S, SL, gw, nw, strip, out);
     }
 }
 
@@ -583,10 +588,11 @@ template <uint32_t T, int G>
 hipError_t launch_gemv_g(const pi_matset &M, const int8_t *aq, const float *ad, const int32_t *as, int32_t *sums,
                          int mode, uint32_t blocks, hipStream_t s) {
     const MatSet S = to_set(M);
-    if (mode == PI_GEMV_OUT) hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_OUT>), dim3(blocks), dim3(64), 0, s, S, aq, ad, as, sums);
+    const dim3 grid((blocks + kGemvThreads / 64 - 1) / (kGemvThreads / 64)), blk(kGemvThreads);   // blocks: wavefronts
+    if (mode == PI_GEMV_OUT) hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_OUT>), grid, blk, 0, s, S, aq, ad, as, sums);
     else if (mode == PI_GEMV_RESIDUAL)
-        hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_RESIDUAL>), dim3(blocks), dim3(64), 0, s, S, aq, ad, as, sums);
-    else hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_SUMS>), dim3(blocks), dim3(64), 0, s, S, aq, ad, as, sums);
+        hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_RESIDUAL>), grid, blk, 0, s, S, aq, ad, as, sums);
+    else hipLaunchKernelGGL((k_gemv<T, G, PI_GEMV_SUMS>), grid, blk, 0, s, S, aq, ad, as, sums);
     return hipGetLastError();
 }
 

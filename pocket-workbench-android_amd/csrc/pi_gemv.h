@@ -181,32 +181,41 @@ __device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t half, uin
 
 // Calls eat(p[i]) for i = 0..n4-1 in order on a float4 row in LDS.  The
 // reads of the next B float4 are in flight while the current B are used; two
-// named buffers, reads at fixed offsets from one address.  p[n4 .. n4 + B)
+// named buffers, reads at fixed offsets from one address.  p[n4 .. n4 + 2B)
 // must be readable LDS (loaded and ignored).
 template <int B, typename F>
 __device__ __forceinline__ void lds_chain4(const float4 *p, uint32_t n4, F &&eat) {
+    float4 a[B], b[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) a[u] = p[u];
     uint32_t i = 0;
-    if (n4 >= 2 * B) {
-        float4 a[B], b[B];
+    for (; i + 2 * B <= n4; i += 2 * B) {
+        const float4 *q = p + i;
 #pragma unroll
-        for (int u = 0; u < B; u++) a[u] = p[u];
-        for (; i + 2 * B <= n4; i += 2 * B) {
-            const float4 *q = p + i;
+        for (int u = 0; u < B; u++) b[u] = q[B + u];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < B; u++) b[u] = q[B + u];
-            __builtin_amdgcn_sched_barrier(0);
+        for (int u = 0; u < B; u++) eat(a[u]);
+        __builtin_amdgcn_sched_barrier(0);   // a is dead before its registers are reloaded
 #pragma unroll
-            for (int u = 0; u < B; u++) eat(a[u]);
-            __builtin_amdgcn_sched_barrier(0);   // a is dead before its registers are reloaded
+        for (int u = 0; u < B; u++) a[u] = q[2 * B + u];
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int u = 0; u < B; u++) a[u] = q[2 * B + u];
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int u = 0; u < B; u++) eat(b[u]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int u = 0; u < B; u++) eat(b[u]);
+        __builtin_amdgcn_sched_barrier(0);
     }
-    for (; i < n4; i++) eat(p[i]);
+    // fewer than 2B left: a already holds p[i .. i + B)
+    const uint32_t rem = n4 - i;
+    if (rem) {
+#pragma unroll
+        for (int u = 0; u < B; u++) b[u] = p[i + B + u];
+#pragma unroll
+        for (int u = 0; u < B; u++)
+            if ((uint32_t)u < rem) eat(a[u]);
+#pragma unroll
+        for (int u = 0; u < B; u++)
+            if ((uint32_t)(B + u) < rem) eat(b[u]);
+    }
 }
 
 // acc = fma(v, v, acc) over the row in order: one accumulator of
@@ -525,17 +534,22 @@ __device__ __forceinline__ void lds_fold4(const float4 *p, uint32_t n4, F &&f) {
     for (uint32_t i = nb * B; i < n4; i++) f(p[i]);
 }
 
+// float4 read ahead per step by the per-row term chains (a wavefront's term
+// strip); the persistent kernel, at its register limit, uses fewer.
+#ifndef PI_CHAIN_B
+#define PI_CHAIN_B 9
+#endif
 // Floats readable after the end of every row a chain_sum reads (strips are
 // followed by this much LDS).
-constexpr uint32_t kChainPad = 32;
+constexpr uint32_t kChainPad = 8 * PI_CHAIN_B + 8;
 
 // Sums n terms of the strip at p strictly left to right, starting from 0.
-// The next 6 float4 are read while the current ones are added (p[n .. n+24)
-// is read ahead and ignored).
+// The next float4 are read while the current ones are added (p[n .. n +
+// 8 * PI_CHAIN_B) is read ahead and ignored).
 __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
     float acc = 0.0f;
     if ((n & 3u) == 0) {
-        lds_chain4<6>(reinterpret_cast<const float4 *>(p), n / 4, [&](const float4 &v) {
+        lds_chain4<PI_CHAIN_B>(reinterpret_cast<const float4 *>(p), n / 4, [&](const float4 &v) {
             acc += v.x;
             acc += v.y;
             acc += v.z;

@@ -26,6 +26,7 @@
 // so the HBM latency of the weights overlaps the hand-off.  The GEMV core,
 // Q8 rule and float orders are those of pi_gemv.h / pi_decode.hip, so the
 // results are bit-identical to the CPU path.
+#define PI_CHAIN_B 6   // per-row chains read 6 float4 ahead (the kernel is at its register limit)
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
@@ -45,7 +46,7 @@ constexpr uint32_t kRedFloats = 512;   // small LDS scratch
 constexpr uint32_t kStripFloats = MW * 64 * 16;
 
 // Row stride of the transposed x (floats).  The rows are followed by at least
-// 24 more floats of the LDS plan (row padding, then the Q8 activation), which
+// 48 more floats of the LDS plan (row padding, then the Q8 activation), which
 // the norm's sum-of-squares chain reads ahead and ignores.
 __host__ __device__ constexpr uint32_t xt_stride(uint32_t ne) { return ne / 8 + 4; }
 __host__ __device__ constexpr uint32_t align16(uint32_t b) { return (b + 15u) & ~15u; }

@@ -459,7 +459,7 @@ __global__ __launch_bounds__(256) void k_pf_embed(const uint8_t *__restrict__ E,
 // ahead); thread 0 adds the squares in order; pairs of lanes then quantize
 // half a block each.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kNormPad = 32;
+constexpr uint32_t kNormPad = 64;
 
 __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X, const float *__restrict__ w,
                                                     uint32_t ne, float eps, pi_pf_q8 o) {
