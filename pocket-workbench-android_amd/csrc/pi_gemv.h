@@ -566,9 +566,10 @@ __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
 // the lane owning it calls out(m, row, value) with value = 0 + sum of terms.
 // Weights of the next tile are requested before the current tile is used
 // (two named buffers, so both stay in registers).
-template <uint32_t T, int G, typename SS, typename Out>
-__device__ __forceinline__ void consume_tile(const SS &S, const Slice<T, G> &A, const Unit<T, G> &U,
-                                             const TileRef &R, float *strip, Out &out) {
+// per_row: terms per row (units per row * TPU).
+template <uint32_t T, int G, typename Out>
+__device__ __forceinline__ void consume_tile_pr(uint32_t per_row, const Slice<T, G> &A, const Unit<T, G> &U,
+                                                const TileRef &R, float *strip, Out &out) {
     constexpr int TPU = QT<T>::TPB * G;
     const uint32_t lane = threadIdx.x & 63u;
     float term[TPU];
@@ -579,9 +580,14 @@ __device__ __forceinline__ void consume_tile(const SS &S, const Slice<T, G> &A, 
         for (int t = 0; t < TPU; t++) strip[lane * TPU + t] = term[t];
     }
     wave_sync();
-    const uint32_t per_row = ms_upr(S) * TPU;
     if (lane < R.nrows) out(R.m, R.row0 + lane, 0.0f + chain_sum(strip + lane * per_row, per_row));
     wave_sync();
+}
+
+template <uint32_t T, int G, typename SS, typename Out>
+__device__ __forceinline__ void consume_tile(const SS &S, const Slice<T, G> &A, const Unit<T, G> &U,
+                                             const TileRef &R, float *strip, Out &out) {
+    consume_tile_pr<T, G>(ms_upr(S) * (QT<T>::TPB * G), A, U, R, strip, out);
 }
 
 // Runs the tiles gt = first, first + stride, ... of S on one wavefront, the

@@ -217,7 +217,8 @@ __host__ __device__ inline LdsPlan lds_plan(uint32_t ne, uint32_t n_ff, uint32_t
     p.strips = p.hb + align16(umax(umax(n_ff, ne) * 4u, 2u * kChunk * kChunkPad * 4u));
     p.red = p.strips + kStripFloats * 4u;
     p.sc = p.red + kRedFloats * 4u;
-    p.total = p.sc + align16(n_ctx * 4u);
+    // whole chunks of e_p, then the chain reader's read-ahead
+    p.total = p.sc + align16((n_ctx + kChunk - 1u) / kChunk * kChunk * 4u) + 256u;
     return p;
 }
 
@@ -339,14 +340,35 @@ __device__ __forceinline__ bool poll_x(const Lds &L, const uint64_t *src, uint32
 // register ring before the stage waits for its input (prefetch_ring), and
 // after tile i is consumed, tile i + P is requested into its slot.
 // ---------------------------------------------------------------------------
+// Geometry of a matrix set that the tiles of a stage need once the input has
+// arrived: total tiles, units per row and this lane's unit within a row.  It
+// is read before the wait and passed through an empty asm, so the compiler
+// keeps the values in registers instead of re-reading the descriptor (a
+// serial chain of scalar-cache misses) after the wait.
+struct Geo {
+    uint32_t nt, upr, ul;
+};
+// A uniform value read from a descriptor, held in registers from here on (see
+// Geo).
+template <typename V> __device__ __forceinline__ V keep(V v) {
+    asm volatile("" : "+s"(v));
+    return v;
+}
+template <typename SS> __device__ __forceinline__ Geo geo_of(const SS &S) {
+    Geo g{ms_total(S), ms_upr(S), 0u};
+    g.ul = (threadIdx.x & 63u) % g.upr;
+    asm volatile("" : "+s"(g.nt), "+s"(g.upr), "+v"(g.ul));
+    return g;
+}
+
 template <uint32_t T, int G, int P, typename SS>
-__device__ __forceinline__ void prefetch_ring(const SS &S, uint32_t first, uint32_t stride, Unit<T, G> (&U)[P],
-                                              TileRef (&R)[P]) {
-    const uint32_t nt = ms_total(S), lane = threadIdx.x & 63u;
+__device__ __forceinline__ void prefetch_ring(const SS &S, const Geo &g, uint32_t first, uint32_t stride,
+                                              Unit<T, G> (&U)[P], TileRef (&R)[P]) {
+    const uint32_t lane = threadIdx.x & 63u;
 #pragma unroll
     for (int k = 0; k < P; k++) {
         const uint32_t gt = first + (uint32_t)k * stride;
-        if (gt < nt) {
+        if (gt < g.nt) {
             R[k] = tile_ref(S, gt);
             U[k].load(R[k].base, R[k].lanes, min(lane, R[k].lanes - 1));
         }
@@ -354,18 +376,18 @@ __device__ __forceinline__ void prefetch_ring(const SS &S, uint32_t first, uint3
 }
 
 template <uint32_t T, int G, int P, typename SS, typename Out>
-__device__ __forceinline__ void gemv_ring(const SS &S, const Lds &L, Unit<T, G> (&U)[P], TileRef (&R)[P],
-                                          uint32_t first, uint32_t stride, Out out) {
-    const uint32_t lane = threadIdx.x & 63u, nt = ms_total(S);
+__device__ __forceinline__ void gemv_ring(const SS &S, const Geo &g, const Lds &L, Unit<T, G> (&U)[P],
+                                          TileRef (&R)[P], uint32_t first, uint32_t stride, Out out) {
+    const uint32_t lane = threadIdx.x & 63u, nt = g.nt, per_row = g.upr * (QT<T>::TPB * G);
     if (first >= nt) return;
     Slice<T, G> SL;
-    SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, lane % ms_upr(S));
+    SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
     uint32_t gt = first;
     for (;;) {
 #pragma unroll
         for (int k = 0; k < P; k++) {
             if (gt >= nt) return;
-            consume_tile<T, G, SS>(S, SL, U[k], R[k], L.strip, out);
+            consume_tile_pr<T, G>(per_row, SL, U[k], R[k], L.strip, out);
             const uint32_t gn = gt + (uint32_t)P * stride;
             if (gn < nt) {
                 R[k] = tile_ref(S, gn);
@@ -423,9 +445,10 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
     const SetRef SA{&Yp->qkv}, SB{&Yp->vb};
     const uint32_t t_qkv = cload(&Yp->t_qkv), t_vb = cload(&Yp->t_vb);
     const float *attn_norm = cload(&Yp->attn_norm);
-    uint64_t *oq = cload(&Yp->q), *okk = cload(&Yp->k), *ov = cload(&Yp->v);
-    const uint32_t ntA = ms_total(SA);
-    const uint32_t ntB = ms_n(SB) ? ms_total(SB) : 0u;
+    uint64_t *oq = keep(cload(&Yp->q)), *okk = keep(cload(&Yp->k)), *ov = keep(cload(&Yp->v));
+    const Geo gA = geo_of(SA);
+    const Geo gB = ms_n(SB) ? geo_of(SB) : Geo{0u, 1u, 0u};
+    const uint32_t ntA = gA.nt, ntB = gB.nt;
     // segment B continues the wavefront numbering after segment A
     const uint32_t firstB = (gw + nw - ntA % nw) % nw;
     with_kq(t_qkv, [&](auto TA_, auto) {
@@ -435,8 +458,8 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             Unit<TB, 1> UB[1];
             TileRef RA[1], RB[1];
             const bool b_first = gw >= ntA && firstB < ntB;   // B is this wavefront's first work
-            if (b_first) prefetch_ring<TB, 1, 1>(SB, firstB, nw, UB, RB);
-            else prefetch_ring<TA, 1, 1>(SA, gw, nw, UA, RA);
+            if (b_first) prefetch_ring<TB, 1, 1>(SB, gB, firstB, nw, UB, RB);
+            else prefetch_ring<TA, 1, 1>(SA, gA, gw, nw, UA, RA);
             float4 wr[4];
             load_norm_w(attn_norm, a.ne, wr);
             lds_barrier();
@@ -452,12 +475,12 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             };
             auto outB = [&](uint32_t, uint32_t row, float v) { ll_put(ov + row, __float_as_uint(v), r.epoch); };
             if (b_first) {
-                gemv_ring<TB, 1, 1>(SB, L, UB, RB, firstB, nw, outB);
+                gemv_ring<TB, 1, 1>(SB, gB, L, UB, RB, firstB, nw, outB);
             } else {
-                gemv_ring<TA, 1, 1>(SA, L, UA, RA, gw, nw, outA);
+                gemv_ring<TA, 1, 1>(SA, gA, L, UA, RA, gw, nw, outA);
                 if (firstB < ntB) {
-                    prefetch_ring<TB, 1, 1>(SB, firstB, nw, UB, RB);
-                    gemv_ring<TB, 1, 1>(SB, L, UB, RB, firstB, nw, outB);
+                    prefetch_ring<TB, 1, 1>(SB, gB, firstB, nw, UB, RB);
+                    gemv_ring<TB, 1, 1>(SB, gB, L, UB, RB, firstB, nw, outB);
                 }
             }
             trace_detail(a, r, 2);
@@ -633,6 +656,10 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
                                     [&](uint32_t i, uint32_t bits) { L.sc[p1 + i] = __uint_as_float(bits); });
         PI_POLL_OR_LEAVE(oke);
     }
+    // e_p = 0 past the last position up to the end of its chunk, so every
+    // chunk is added whole: both sums start at +0 and never become -0, so
+    // adding +0 leaves them unchanged.
+    for (uint32_t p = n + tid; p < nchunk * kChunk; p += MT) L.sc[p] = 0.0f;
     lds_barrier();
     trace_detail(a, r, 4);
 
@@ -642,13 +669,14 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     // 16-byte load) and keep the V rows of the next kDepth chunks in flight
     // in registers; wavefront 0 adds chunk c - 1 in order while chunk c is
     // being formed.  V rows always come from HBM (rows past the end re-read
-    // row n-1); the current position's row is taken from LDS.
+    // row n-1, whose product is 0 since e_p = 0 there); the current
+    // position's row is taken from LDS.
     auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
         float *buf = L.hb + (c & 1u) * kChunk * kChunkPad;
 #pragma unroll
         for (int i = 0; i < GPW; i++) {
             const uint32_t g = (wave - 1) + (MW - 1) * i, rr = 4 * g + sub, p = c * kChunk + rr;
-            if (g < kChunk / 4 && p < n) {
+            if (g < kChunk / 4) {
                 const float e = L.sc[p];
                 const float4 vv = p == (uint32_t)pos ? vme : v[i];
                 buf[(d0 + 0) * kChunkPad + rr] = (e != 0.0f) ? e * vv.x : 0.0f;
@@ -669,47 +697,23 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
                     store_products(c, vr[k]);
                     if (c + kDepth < nchunk) load_v(c + kDepth, vr[k]);
                     if (wave == MW - 1 && lane == 0) {
-                        const uint32_t p0 = c * kChunk, rows = min(kChunk, n - p0);
-                        if (rows == kChunk) {
-                            const float4 *e4 = reinterpret_cast<const float4 *>(L.sc + p0);
-#pragma unroll
-                            for (uint32_t q = 0; q < kChunk / 4; q += 4) {
-                                float4 t[4];
-#pragma unroll
-                                for (int u = 0; u < 4; u++) t[u] = e4[q + u];
-#pragma unroll
-                                for (int u = 0; u < 4; u++) {
-                                    sum += t[u].x;
-                                    sum += t[u].y;
-                                    sum += t[u].z;
-                                    sum += t[u].w;
-                                }
-                            }
-                        } else {
-                            for (uint32_t q = 0; q < rows; q++) sum += L.sc[p0 + q];
-                        }
+                        lds_chain4<4>(reinterpret_cast<const float4 *>(L.sc + c * kChunk), kChunk / 4,
+                                      [&](const float4 &t) {
+                                          sum += t.x;
+                                          sum += t.y;
+                                          sum += t.z;
+                                          sum += t.w;
+                                      });
                     }
                 }
             } else if (c >= 1) {
-                const uint32_t cc = c - 1, rows = min(kChunk, n - cc * kChunk);
-                const float *row = L.hb + (cc & 1u) * kChunk * kChunkPad + lane * kChunkPad;
-                if (rows == kChunk) {
-#pragma unroll
-                    for (uint32_t q = 0; q < kChunk; q += 16) {
-                        float4 t[4];
-#pragma unroll
-                        for (int u = 0; u < 4; u++) t[u] = reinterpret_cast<const float4 *>(row + q)[u];
-#pragma unroll
-                        for (int u = 0; u < 4; u++) {
-                            acc = acc + t[u].x;
-                            acc = acc + t[u].y;
-                            acc = acc + t[u].z;
-                            acc = acc + t[u].w;
-                        }
-                    }
-                } else {
-                    for (uint32_t q = 0; q < rows; q++) acc = acc + row[q];
-                }
+                const float *row = L.hb + ((c - 1) & 1u) * kChunk * kChunkPad + lane * kChunkPad;
+                lds_chain4<4>(reinterpret_cast<const float4 *>(row), kChunk / 4, [&](const float4 &t) {
+                    acc = acc + t.x;
+                    acc = acc + t.y;
+                    acc = acc + t.z;
+                    acc = acc + t.w;
+                });
             }
             lds_barrier();
         }
@@ -748,13 +752,14 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
     const SetRef SO{&Yp->o};
     const uint32_t t_o = cload(&Yp->t_o), g_o = cload(&Yp->g_o);
     const uint64_t *yatt = cload(&Yp->att);
-    uint64_t *yxb = cload(&Yp->xb);
+    uint64_t *yxb = keep(cload(&Yp->xb));
     with_any(t_o, g_o, [&](auto T_, auto G_) {
         constexpr uint32_t T = decltype(T_)::value;
         constexpr int G = decltype(G_)::value;
         Unit<T, G> U[1];
         TileRef R[1];
-        prefetch_ring<T, G, 1>(SO, gw, nw, U, R);
+        const Geo g = geo_of(SO);
+        prefetch_ring<T, G, 1>(SO, g, gw, nw, U, R);
         lds_barrier();
         const uint32_t nwords = qdim / 4 + qdim / 16;
         ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag,
@@ -763,7 +768,7 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxb + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
         };
-        gemv_ring<T, G, 1>(SO, L, U, R, gw, nw, out);
+        gemv_ring<T, G, 1>(SO, g, L, U, R, gw, nw, out);
     });
     if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
     return ok;
@@ -781,12 +786,13 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
     const uint32_t t_gu = cload(&Yp->t_gu);
     const float *ffn_norm = cload(&Yp->ffn_norm);
     const uint64_t *yxb = cload(&Yp->xb);
-    uint64_t *yh = cload(&Yp->h);
+    uint64_t *yh = keep(cload(&Yp->h));
     with_kq(t_gu, [&](auto T_, auto) {
         constexpr uint32_t T = decltype(T_)::value;
         constexpr int TPU = QT<T>::TPB;
         const uint32_t lane = threadIdx.x & 63u;
         const SetRef &S = SGU;
+        const Geo g = geo_of(S);
         const uint32_t npair = ms_t0(S, 1);
         const uint32_t p0 = gw;
         Unit<T, 1> Ug, Uu;
@@ -807,8 +813,8 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
         trace_detail(a, r, 7);
         if (gw >= npair) return;
         Slice<T, 1> SL;
-        SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, lane % ms_upr(S));
-        const uint32_t per_row = ms_upr(S) * TPU;
+        SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+        const uint32_t per_row = g.upr * TPU;
         for (uint32_t p = gw; p < npair; p += nw) {
             if (p != p0) {
                 Rg = tile_ref(S, p);
@@ -856,13 +862,14 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
     const SetRef SD{&Yp->down};
     const uint32_t t_down = cload(&Yp->t_down), g_down = cload(&Yp->g_down);
     const uint64_t *yh = cload(&Yp->h);
-    uint64_t *yxo = cload(&Yp->xo);
+    uint64_t *yxo = keep(cload(&Yp->xo));
     with_any(t_down, g_down, [&](auto T_, auto G_) {
         constexpr uint32_t T = decltype(T_)::value;
         constexpr int G = decltype(G_)::value;
         Unit<T, G> U[3];
         TileRef R[3];
-        prefetch_ring<T, G, 3>(SD, gw, nw, U, R);
+        const Geo g = geo_of(SD);
+        prefetch_ring<T, G, 3>(SD, g, gw, nw, U, R);
         lds_barrier();
         ok = wg_poll<23>(yh, a.n_ff, r.epoch, a.abort_flag,
                          [&](uint32_t i, uint32_t bits) { L.hb[i] = __uint_as_float(bits); });
@@ -887,7 +894,7 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxo + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
         };
-        gemv_ring<T, G, 3>(SD, L, U, R, gw, nw, out);
+        gemv_ring<T, G, 3>(SD, g, L, U, R, gw, nw, out);
         trace_detail(a, r, 11);
         trace_clock(a, r, 15);
     });
@@ -919,7 +926,8 @@ __device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, c
         constexpr uint32_t T = decltype(T_)::value;
         Unit<T, 1> U[2];
         TileRef R[2];
-        prefetch_ring<T, 1, 2>(SH, gw, nw, U, R);
+        const Geo g = geo_of(SH);
+        prefetch_ring<T, 1, 2>(SH, g, gw, nw, U, R);
         float4 wr[4];
         load_norm_w(a.out_norm, a.ne, wr);
         lds_barrier();
@@ -930,7 +938,7 @@ __device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, c
             gst(a.logits)[row] = v;
             amax_merge(best_v, best_i, v, row);
         };
-        gemv_ring<T, 1, 2>(SH, L, U, R, gw, nw, out);
+        gemv_ring<T, 1, 2>(SH, g, L, U, R, gw, nw, out);
     });
     if (!ok) {
         if (threadIdx.x == 0) raise_abort(a.abort_flag);
