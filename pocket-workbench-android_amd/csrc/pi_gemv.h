@@ -62,6 +62,17 @@ template <> struct QT<PI_TYPE_Q6_K> { static constexpr int BE = 256, BC = 13, DF
 template <> struct QT<PI_TYPE_Q4_0> { static constexpr int BE = 32, BC = 1, DF = 1, TPB = 1; };
 template <> struct QT<PI_TYPE_Q8_0> { static constexpr int BE = 32, BC = 2, DF = 1, TPB = 1; };
 
+// clamp(round(y), -127, 127) with round half away from zero, NaN -> 0
+// (quant_int.rs:49: (x * inv).round().clamp(-127.0, 127.0) as i32).
+// round(y) == trunc(y + copysign(0.5 - 2^-25, y)) for every float |y| < 2^22
+// (the sum rounds up past the next integer exactly when the fraction is at
+// least one half); clamping the sum to +-127 before truncation gives the same
+// clamp, and larger |y| only ever clamps.
+__device__ __forceinline__ int q8_round_clamp(float y) {
+    const float r = __builtin_amdgcn_fmed3f(y + __builtin_copysignf(0.49999997f, y), -127.0f, 127.0f);
+    return (y != y) ? 0 : (int)r;
+}
+
 // ---------------------------------------------------------------------------
 // Q8 quantization of one 32-element block held by one lane (quant_int.rs:33-55):
 // amax ignores NaN; d = amax/127 and inv = 1/d correctly rounded; roundf is
@@ -83,10 +94,7 @@ __device__ __forceinline__ void q8_lane(const float (&v)[32], uint32_t *qw, floa
         uint32_t word = 0;
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            float r = roundf(v[4 * w + b] * inv);
-            if (r < -127.0f) r = -127.0f;
-            if (r > 127.0f) r = 127.0f;
-            const int iv = (r != r) ? 0 : (int)r;
+            const int iv = q8_round_clamp(v[4 * w + b] * inv);
             s += iv;
             word |= ((uint32_t)iv & 0xFFu) << (8 * b);
         }
@@ -105,10 +113,7 @@ __device__ __forceinline__ int q8_block32_core(float v, float &dd, int &sum) {
     for (int off = 16; off; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
     dd = a / 127.0f;
     const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
-    float r = roundf(v * inv);
-    if (r < -127.0f) r = -127.0f;
-    if (r > 127.0f) r = 127.0f;
-    const int iv = (r != r) ? 0 : (int)r;
+    const int iv = q8_round_clamp(v * inv);
     int s = iv;
 #pragma unroll
     for (int off = 16; off; off >>= 1) s += __shfl_xor(s, off, 32);
@@ -145,24 +150,16 @@ __device__ __forceinline__ void q8_pair_core(const float (&v)[16], uint32_t (&qw
     const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
     int iv[16];
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        float r = roundf(v[j] * inv);
-        if (r < -127.0f) r = -127.0f;
-        if (r > 127.0f) r = 127.0f;
-        iv[j] = (r != r) ? 0 : (int)r;
-    }
+    for (int j = 0; j < 16; j++) iv[j] = q8_round_clamp(v[j] * inv);
 #pragma unroll
     for (int w = 0; w < 4; w++)
         qw[w] = ((uint32_t)iv[4 * w] & 0xFFu) | (((uint32_t)iv[4 * w + 1] & 0xFFu) << 8) |
                 (((uint32_t)iv[4 * w + 2] & 0xFFu) << 16) | (((uint32_t)iv[4 * w + 3] & 0xFFu) << 24);
-    int t[8];
+    // block sum of the 16 quants (exact integer dot products with 1)
+    int t = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) t[j] = iv[2 * j] + iv[2 * j + 1];
-#pragma unroll
-    for (int w = 4; w; w >>= 1)
-#pragma unroll
-        for (int j = 0; j < w; j++) t[j] += t[j + w];
-    sum = t[0] + __shfl_xor(t[0], 1, 64);
+    for (int w = 0; w < 4; w++) t = sdot4((int)qw[w], 0x01010101, t);
+    sum = t + __shfl_xor(t, 1, 64);
 }
 // Writes this half's 4 quant words to qw; the even lane writes d and the sum.
 __device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t half, uint32_t *qw, float *dout,

@@ -59,6 +59,29 @@ def test_q8_quantize_halfway_vector(pih, backend, oracle):
     assert np.array_equal(s, ref.sum)
 
 
+def test_q8_quantize_every_tie(pih, backend, oracle):
+    """Every exact tie k + 0.5 in (-127, 127) and both float neighbours of each
+    tie: blocks whose maximum is 127, so d = 1 and inv = 1 (quant_int.rs:41-49)."""
+    ties = np.arange(-127, 127, dtype=np.float32) + np.float32(0.5)
+    vals = np.concatenate([ties, np.nextafter(ties, np.float32(-np.inf)), np.nextafter(ties, np.float32(np.inf))])
+    per = 31
+    nb = -(-vals.size // per)
+    x = np.zeros((nb, 32), np.float32)
+    x[:, 0] = 127.0
+    flat = np.zeros(nb * per, np.float32)
+    flat[: vals.size] = vals
+    x[:, 1:] = flat.reshape(nb, per)
+    k = 32 * nb
+    x = x.reshape(-1)
+    q, d, s = backend.q8_quantize(x, k, 1)
+    ref = oracle.Act(x, k, 1)
+    assert np.all(d == 1.0)
+    assert np.array_equal(q, ref.q)
+    assert np.array_equal(s, ref.sum)
+    tie_q = q.reshape(nb, 32)[:, 1:].reshape(-1)[: ties.size]
+    assert np.array_equal(tie_q, np.where(ties > 0, np.ceil(ties), np.floor(ties)).astype(np.int8))
+
+
 CASES = [
     (Q4_K, 5760, 2304),     # config 1 shape
     (Q4_K, 2304, 2304),     # attn_q/k/o
