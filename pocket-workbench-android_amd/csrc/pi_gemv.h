@@ -62,6 +62,91 @@ template <> struct QT<PI_TYPE_Q6_K> { static constexpr int BE = 256, BC = 13, DF
 template <> struct QT<PI_TYPE_Q4_0> { static constexpr int BE = 32, BC = 1, DF = 1, TPB = 1; };
 template <> struct QT<PI_TYPE_Q8_0> { static constexpr int BE = 32, BC = 2, DF = 1, TPB = 1; };
 
+// ---------------------------------------------------------------------------
+// Lane exchanges through DPP moves (a VALU operand modifier, no LDS round
+// trip).  Every lane that is read must be active.
+// ---------------------------------------------------------------------------
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each row of 16
+constexpr int kDppBcast15 = 0x142;     // lane 15 of row r -> row r + 1
+constexpr int kDppBcast31 = 0x143;     // lane 31 -> rows 2 and 3
+template <int CTRL, int ROWS = 0xF> __device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS = 0xF> __device__ __forceinline__ uint32_t dpp(uint32_t v) {
+    return (uint32_t)dpp<CTRL, ROWS>((int)v);
+}
+template <int CTRL, int ROWS = 0xF> __device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(dpp<CTRL, ROWS>(__float_as_int(v)));
+}
+// op over each row of 16 lanes, in every lane of the row (op commutative and
+// associative on the values it sees, e.g. max or integer add).
+template <typename T, typename Op> __device__ __forceinline__ T row16_allreduce(T v, Op op) {
+    v = op(v, dpp<kDppXor1>(v));
+    v = op(v, dpp<kDppXor2>(v));
+    v = op(v, dpp<kDppHalfMirror>(v));
+    v = op(v, dpp<kDppMirror>(v));
+    return v;
+}
+// ... over each group of 32 lanes (ds_swizzle xor 16 for the last step).
+template <typename T, typename Op> __device__ __forceinline__ T half32_allreduce(T v, Op op) {
+    v = row16_allreduce(v, op);
+    int o;
+    if constexpr (sizeof(T) == 4) {
+        int b;
+        __builtin_memcpy(&b, &v, 4);
+        o = __builtin_amdgcn_ds_swizzle(b, 0x401F);   // bit mode: and 0x1F, xor 0x10
+        T t;
+        __builtin_memcpy(&t, &o, 4);
+        v = op(v, t);
+    }
+    return v;
+}
+// DPP move whose lanes outside ROWS receive `old`.
+template <int CTRL, int ROWS> __device__ __forceinline__ float dpp_or(float old, float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), CTRL, ROWS, 0xF, false));
+}
+template <int CTRL, int ROWS> __device__ __forceinline__ uint32_t dpp_or(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
+}
+// Maximum over the whole wavefront (every lane active), returned in every
+// lane: rows of 16 first, then lane 63 collects the rows through row
+// broadcasts and is read as a scalar.
+__device__ __forceinline__ float wave_max(float v) {
+    auto mx = [](float x, float y) { return fmaxf(x, y); };
+    v = row16_allreduce(v, mx);
+    v = fmaxf(v, dpp_or<kDppBcast15, 0xA>(v, v));
+    v = fmaxf(v, dpp_or<kDppBcast31, 0xC>(v, v));
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+// (value, index) with the larger value, the smaller index on equal values.
+__device__ __forceinline__ void argmax_merge(float &bv, uint32_t &bi, float v, uint32_t i) {
+    if (v > bv || (v == bv && i < bi)) {
+        bv = v;
+        bi = i;
+    }
+}
+template <int CTRL, int ROWS = 0xF> __device__ __forceinline__ void argmax_step(float &v, uint32_t &i) {
+    const float ov = dpp_or<CTRL, ROWS>(v, v);
+    const uint32_t oi = dpp_or<CTRL, ROWS>(i, i);
+    argmax_merge(v, i, ov, oi);
+}
+// argmax_merge over the whole wavefront (every lane active); the result in
+// every lane.  The merge picks one pair by a total order, so the grouping of
+// the steps does not change the result.
+__device__ __forceinline__ void wave_argmax(float &v, uint32_t &i) {
+    argmax_step<kDppXor1>(v, i);
+    argmax_step<kDppXor2>(v, i);
+    argmax_step<kDppHalfMirror>(v, i);
+    argmax_step<kDppMirror>(v, i);
+    argmax_step<kDppBcast15, 0xA>(v, i);
+    argmax_step<kDppBcast31, 0xC>(v, i);
+    v = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+    i = (uint32_t)__builtin_amdgcn_readlane((int)i, 63);
+}
+
 // clamp(round(y), -127, 127) with round half away from zero, NaN -> 0
 // (quant_int.rs:49: (x * inv).round().clamp(-127.0, 127.0) as i32).
 // round(y) == trunc(y + copysign(0.5 - 2^-25, y)) for every float |y| < 2^22
@@ -109,15 +194,11 @@ __device__ __forceinline__ void q8_lane(const float (&v)[32], uint32_t *qw, floa
 // Returns this lane's quant; d and the block sum are returned in every lane.
 __device__ __forceinline__ int q8_block32_core(float v, float &dd, int &sum) {
     float a = (v == v) ? fabsf(v) : 0.0f;
-#pragma unroll
-    for (int off = 16; off; off >>= 1) a = fmaxf(a, __shfl_xor(a, off, 32));
+    a = half32_allreduce(a, [](float x, float y) { return fmaxf(x, y); });
     dd = a / 127.0f;
     const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
     const int iv = q8_round_clamp(v * inv);
-    int s = iv;
-#pragma unroll
-    for (int off = 16; off; off >>= 1) s += __shfl_xor(s, off, 32);
-    sum = s;
+    sum = half32_allreduce(iv, [](int x, int y) { return x + y; });
     return iv;
 }
 __device__ __forceinline__ void q8_block32(float v, int j, int8_t *qout, float *dout, int32_t *sout, bool store) {
@@ -144,7 +225,7 @@ __device__ __forceinline__ void q8_pair_core(const float (&v)[16], uint32_t (&qw
     for (int w = 4; w; w >>= 1)
 #pragma unroll
         for (int j = 0; j < w; j++) m[j] = fmaxf(m[j], m[j + w]);
-    float amax = fmaxf(m[0], __shfl_xor(m[0], 1, 64));
+    float amax = fmaxf(m[0], dpp<kDppXor1>(m[0]));
     amax = fmaxf(amax, 0.0f);   // all-NaN block: 0
     dd = amax / 127.0f;
     const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
@@ -159,7 +240,7 @@ __device__ __forceinline__ void q8_pair_core(const float (&v)[16], uint32_t (&qw
     int t = 0;
 #pragma unroll
     for (int w = 0; w < 4; w++) t = sdot4((int)qw[w], 0x01010101, t);
-    sum = t + __shfl_xor(t, 1, 64);
+    sum = t + dpp<kDppXor1>(t);
 }
 // Writes this half's 4 quant words to qw; the even lane writes d and the sum.
 __device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t half, uint32_t *qw, float *dout,

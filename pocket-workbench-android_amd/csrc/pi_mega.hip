@@ -625,8 +625,7 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         L.sc[pos] = s;
         mx = fmaxf(mx, s);
     }
-#pragma unroll
-    for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    mx = wave_max(mx);
     if (lane == 0) misc[wave] = mx;
     lds_barrier();
     mx = fmaxf(fmaxf(misc[0], misc[1]), fmaxf(misc[2], misc[3]));
@@ -945,12 +944,7 @@ __device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, c
         return false;
     }
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-#pragma unroll
-    for (int off = 32; off; off >>= 1) {
-        const float ov = __shfl_xor(best_v, off, 64);
-        const uint32_t oi = __shfl_xor(best_i, off, 64);
-        amax_merge(best_v, best_i, ov, oi);
-    }
+    wave_argmax(best_v, best_i);
     float *sv = L.red + 400;
     uint32_t *si = reinterpret_cast<uint32_t *>(L.red + 408);
     if (lane == 0) {
@@ -975,12 +969,7 @@ __device__ __forceinline__ bool stage_head(const Cfg &a, Run r, const Lds &Lc, c
         amax_merge(bv, bi, __uint_as_float((uint32_t)wv), (uint32_t)wi);
     }
     PI_POLL_OR_LEAVE(ok);
-#pragma unroll
-    for (int off = 32; off; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const uint32_t oi = __shfl_xor(bi, off, 64);
-        amax_merge(bv, bi, ov, oi);
-    }
+    wave_argmax(bv, bi);
     if (lane == 0) {
         sv[wave] = bv;
         si[wave] = bi;
