@@ -456,7 +456,8 @@ pig::MatSet mset(std::initializer_list<const pi_tensor *> ts) {
 int build_mega(pi_ctx *c, Engine &e) {
     e.mega_ok = false;
     const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
-    if (e.n_embd % 128 || e.n_embd / 16 > 256 || e.n_ff / 32 > 256 || e.n_rot / 2 > 32 || e.dh != 64 || e.n_layer > 63)
+    if (e.n_embd % 128 || e.n_ff % 128 || (e.n_head * e.dh) % 128 || e.n_embd / 16 > 256 || e.n_ff / 32 > 256 ||
+        e.n_rot / 2 > 32 || e.dh != 64 || e.n_layer > 63)
         return PI_OK;
     int maxlds = 0;
     if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;

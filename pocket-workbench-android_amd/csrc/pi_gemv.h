@@ -324,6 +324,13 @@ __device__ __forceinline__ float sumsq_scalar_chain(const float4 *p, uint32_t n4
     return acc;
 }
 
+// Position of 16-byte chunk k of a Q8 activation kept in LDS.  Within each
+// 256-byte row r the chunks are permuted by c -> c ^ (r & 7), so lanes that
+// read the same chunk of different rows (one unit each) hit different banks
+// instead of all queueing on the same four.  With activation lengths that are
+// multiples of 128, a final half row (8 chunks) maps onto itself.
+__device__ __forceinline__ uint32_t act_chunk(uint32_t k) { return k ^ ((k >> 4) & 7u); }
+
 // ---------------------------------------------------------------------------
 // Activation slice of one unit (G base blocks) in registers.
 // ---------------------------------------------------------------------------
@@ -341,6 +348,16 @@ template <uint32_t T, int G> struct Slice {
         const int4 *ap = reinterpret_cast<const int4 *>(q + (uint64_t)u * BE * G);
 #pragma unroll
         for (int i = 0; i < AI4; i++) a[i] = ap[i];
+        load_scales(d, s, u);
+    }
+    // The same from an LDS activation whose quant chunks are in act_chunk order.
+    __device__ __forceinline__ void load_swz(const int8_t *q, const float *d, const int32_t *s, uint32_t u) {
+        const int4 *ap = reinterpret_cast<const int4 *>(q);
+#pragma unroll
+        for (int i = 0; i < AI4; i++) a[i] = ap[act_chunk(u * AI4 + (uint32_t)i)];
+        load_scales(d, s, u);
+    }
+    __device__ __forceinline__ void load_scales(const float *d, const int32_t *s, uint32_t u) {
 #pragma unroll
         for (int i = 0; i < NQ8; i++) {
             ad[i] = d[u * NQ8 + i];

@@ -188,7 +188,7 @@ __device__ __forceinline__ float comp4(const float4 &v, int i) { return i == 0 ?
 // LDS of a workgroup
 // ---------------------------------------------------------------------------
 struct QAct {        // Q8 activation of k elements (quant_int.rs:3-14)
-    uint32_t *qw;    // k/4 words of quants
+    uint32_t *qw;    // k/4 words of quants, 16-byte chunks in act_chunk order
     float *d;        // k/32 block scales
     int32_t *s;      // k/32 block sums
 };
@@ -315,7 +315,7 @@ __device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, co
             v[c] = t.x * s * comp4(wr[c / 4], c % 4);
             v[8 + c] = t.y * s * comp4(wr[2 + c / 4], c % 4);
         }
-        q8_pair(v, h, L.act.qw + 8 * b + 4 * h, L.act.d + b, L.act.s + b);
+        q8_pair(v, h, L.act.qw + 4 * act_chunk(2 * b + h), L.act.d + b, L.act.s + b);
     }
     lds_barrier();
 }
@@ -381,7 +381,7 @@ __device__ __forceinline__ void gemv_ring(const SS &S, const Geo &g, const Lds &
     const uint32_t lane = threadIdx.x & 63u, nt = g.nt, per_row = g.upr * (QT<T>::TPB * G);
     if (first >= nt) return;
     Slice<T, G> SL;
-    SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+    SL.load_swz(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
     uint32_t gt = first;
     for (;;) {
 #pragma unroll
@@ -760,9 +760,10 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
         const Geo g = geo_of(SO);
         prefetch_ring<T, G, 1>(SO, g, gw, nw, U, R);
         lds_barrier();
-        const uint32_t nwords = qdim / 4 + qdim / 16;
-        ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag,
-                        [&](uint32_t i, uint32_t bits) { L.act.qw[i] = bits; });
+        const uint32_t nwords = qdim / 4 + qdim / 16, nq = qdim / 4;
+        ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag, [&](uint32_t i, uint32_t bits) {
+            L.act.qw[i < nq ? 4 * act_chunk(i >> 2) + (i & 3u) : i] = bits;
+        });
         if (wg_any(!ok, L.vote)) { ok = false; return; }
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxb + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
@@ -812,7 +813,7 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
         trace_detail(a, r, 7);
         if (gw >= npair) return;
         Slice<T, 1> SL;
-        SL.load(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+        SL.load_swz(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
         const uint32_t per_row = g.upr * TPU;
         for (uint32_t p = gw; p < npair; p += nw) {
             if (p != p0) {
@@ -886,7 +887,7 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
                 v[4 * j4 + 2] = q.z;
                 v[4 * j4 + 3] = q.w;
             }
-            q8_pair(v, h, L.act.qw + 8 * b + 4 * h, L.act.d + b, L.act.s + b);
+            q8_pair(v, h, L.act.qw + 4 * act_chunk(2 * b + h), L.act.d + b, L.act.s + b);
         }
         lds_barrier();
         trace_detail(a, r, 10);
