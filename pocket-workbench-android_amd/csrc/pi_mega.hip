@@ -612,10 +612,11 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         }
     };
     // the chain workgroup requests its first V rows before the softmax
+    // (unconditionally: load_v clamps to row n - 1, and a fixed number of
+    // loads per ring slot lets the compiler wait for the oldest slot only)
     if (seg == 0 && wave != 0) {
 #pragma unroll
-        for (int k = 0; k < kDepth; k++)
-            if ((uint32_t)k < nchunk) load_v(k, vr[k]);
+        for (int k = 0; k < kDepth; k++) load_v(k, vr[k]);
     }
     if (seg == nseg - 1 && tid == ((uint32_t)pos - p0) % MT) {
         float4 kc4[16];
@@ -686,26 +687,49 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         }
     };
     float acc = 0.0f, sum = 0.0f;
-    for (uint32_t c0 = 0; c0 <= nchunk; c0 += kDepth) {
+    // Step c (0..nchunk): wavefronts 1-3 store the products of chunk c and
+    // refill the ring slot they used with the rows of chunk c + kDepth;
+    // wavefront 0 adds chunk c - 1.  Producers and adder run separate loops
+    // with the same barrier count.  In the producers' main loop every step of
+    // a group issues the same loads (rows past the end re-read row n - 1), so
+    // each ring slot keeps its own registers and a wavefront waits only for its
+    // oldest slot while the others stay in flight; the last steps, whose rows
+    // are already requested, run without refills.
+    auto sum_e = [&](uint32_t c) {
+        if (wave == MW - 1 && lane == 0) {
+            lds_chain4<4>(reinterpret_cast<const float4 *>(L.sc + c * kChunk), kChunk / 4, [&](const float4 &t) {
+                sum += t.x;
+                sum += t.y;
+                sum += t.z;
+                sum += t.w;
+            });
+        }
+    };
+    if (wave != 0) {
+        uint32_t c0 = 0;
+        for (; c0 + kDepth <= nchunk; c0 += kDepth) {
 #pragma unroll
-        for (int k = 0; k < kDepth; k++) {
+            for (int k = 0; k < kDepth; k++) {
+                const uint32_t c = c0 + k;
+                store_products(c, vr[k]);
+                load_v(c + kDepth, vr[k]);
+                sum_e(c);
+                lds_barrier();
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kDepth; k++) {   // steps c0 .. nchunk (at most kDepth of them)
             const uint32_t c = c0 + k;
-            if (c > nchunk) break;
-            if (wave != 0) {
-                if (c < nchunk) {
-                    store_products(c, vr[k]);
-                    if (c + kDepth < nchunk) load_v(c + kDepth, vr[k]);
-                    if (wave == MW - 1 && lane == 0) {
-                        lds_chain4<4>(reinterpret_cast<const float4 *>(L.sc + c * kChunk), kChunk / 4,
-                                      [&](const float4 &t) {
-                                          sum += t.x;
-                                          sum += t.y;
-                                          sum += t.z;
-                                          sum += t.w;
-                                      });
-                    }
-                }
-            } else if (c >= 1) {
+            if (c > nchunk) continue;   // uniform over the workgroup
+            if (c < nchunk) {
+                store_products(c, vr[k]);
+                sum_e(c);
+            }
+            lds_barrier();
+        }
+    } else {
+        for (uint32_t c = 0; c <= nchunk; c++) {
+            if (c >= 1) {
                 const float *row = L.hb + ((c - 1) & 1u) * kChunk * kChunkPad + lane * kChunkPad;
                 lds_chain4<4>(reinterpret_cast<const float4 *>(row), kChunk / 4, [&](const float4 &t) {
                     acc = acc + t.x;
