@@ -41,7 +41,7 @@ constexpr uint32_t MT = 256;           // threads per workgroup
 constexpr uint32_t MW = MT / 64;       // wavefronts per workgroup
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr uint32_t kChunk = 64;        // attention positions per product chunk
-constexpr uint32_t kChunkPad = 68;     // floats per dimension row of a chunk (16-byte aligned)
+constexpr uint32_t kChunkPad = 88;     // floats per dimension row of a chunk (16-byte aligned)
 constexpr uint32_t kRedFloats = 512;   // small LDS scratch
 constexpr uint32_t kStripFloats = MW * 64 * 16;
 
@@ -671,40 +671,44 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     // being formed.  V rows always come from HBM (rows past the end re-read
     // row n-1, whose product is 0 since e_p = 0 there); the current
     // position's row is taken from LDS.
+    // Product (d, p) of a chunk is at row d, float4 group (p / 4) ^ ((d / 8) & 7):
+    // the row pitch and the group permutation keep both the producers' single
+    // float stores (16 dimensions of one position per 16 lanes) and the
+    // adder's float4 reads (one row per lane) on distinct banks.
     auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
         float *buf = L.hb + (c & 1u) * kChunk * kChunkPad;
+        const uint32_t hq = (lane & 15u) >> 1;   // (d / 8) & 7 for d = d0 .. d0 + 3
+        float e[GPW];
+#pragma unroll
+        for (int i = 0; i < GPW; i++) {   // all weights first, so their reads overlap
+            const uint32_t g = (wave - 1) + (MW - 1) * i;
+            e[i] = L.sc[c * kChunk + min(4 * g + sub, kChunk - 1)];
+        }
 #pragma unroll
         for (int i = 0; i < GPW; i++) {
-            const uint32_t g = (wave - 1) + (MW - 1) * i, rr = 4 * g + sub, p = c * kChunk + rr;
+            const uint32_t g = (wave - 1) + (MW - 1) * i;
             if (g < kChunk / 4) {
-                const float e = L.sc[p];
+                const uint32_t p = c * kChunk + 4 * g + sub, col = 4 * (g ^ hq) + sub;
                 const float4 vv = p == (uint32_t)pos ? vme : v[i];
-                buf[(d0 + 0) * kChunkPad + rr] = (e != 0.0f) ? e * vv.x : 0.0f;
-                buf[(d0 + 1) * kChunkPad + rr] = (e != 0.0f) ? e * vv.y : 0.0f;
-                buf[(d0 + 2) * kChunkPad + rr] = (e != 0.0f) ? e * vv.z : 0.0f;
-                buf[(d0 + 3) * kChunkPad + rr] = (e != 0.0f) ? e * vv.w : 0.0f;
+                const bool nz = e[i] != 0.0f;
+                buf[(d0 + 0) * kChunkPad + col] = nz ? e[i] * vv.x : 0.0f;
+                buf[(d0 + 1) * kChunkPad + col] = nz ? e[i] * vv.y : 0.0f;
+                buf[(d0 + 2) * kChunkPad + col] = nz ? e[i] * vv.z : 0.0f;
+                buf[(d0 + 3) * kChunkPad + col] = nz ? e[i] * vv.w : 0.0f;
             }
         }
     };
     float acc = 0.0f, sum = 0.0f;
     // Step c (0..nchunk): wavefronts 1-3 store the products of chunk c and
     // refill the ring slot they used with the rows of chunk c + kDepth;
-    // wavefront 0 adds chunk c - 1.  Producers and adder run separate loops
-    // with the same barrier count.  In the producers' main loop every step of
-    // a group issues the same loads (rows past the end re-read row n - 1), so
-    // each ring slot keeps its own registers and a wavefront waits only for its
-    // oldest slot while the others stay in flight; the last steps, whose rows
-    // are already requested, run without refills.
-    auto sum_e = [&](uint32_t c) {
-        if (wave == MW - 1 && lane == 0) {
-            lds_chain4<4>(reinterpret_cast<const float4 *>(L.sc + c * kChunk), kChunk / 4, [&](const float4 &t) {
-                sum += t.x;
-                sum += t.y;
-                sum += t.z;
-                sum += t.w;
-            });
-        }
-    };
+    // wavefront 0 adds chunk c - 1 (lane = dimension) and, in every lane, the
+    // weights of that chunk into the sum of e_p (two independent chains).
+    // Producers and adder run separate loops with the same barrier count.  In
+    // the producers' main loop every step of a group issues the same loads
+    // (rows past the end re-read row n - 1), so each ring slot keeps its own
+    // registers and a wavefront waits only for its oldest slot while the
+    // others stay in flight; the last steps, whose rows are already
+    // requested, run without refills.
     if (wave != 0) {
         uint32_t c0 = 0;
         for (; c0 + kDepth <= nchunk; c0 += kDepth) {
@@ -713,7 +717,6 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
                 const uint32_t c = c0 + k;
                 store_products(c, vr[k]);
                 load_v(c + kDepth, vr[k]);
-                sum_e(c);
                 lds_barrier();
             }
         }
@@ -721,27 +724,41 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         for (int k = 0; k < kDepth; k++) {   // steps c0 .. nchunk (at most kDepth of them)
             const uint32_t c = c0 + k;
             if (c > nchunk) continue;   // uniform over the workgroup
-            if (c < nchunk) {
-                store_products(c, vr[k]);
-                sum_e(c);
-            }
+            if (c < nchunk) store_products(c, vr[k]);
             lds_barrier();
         }
     } else {
+        const uint32_t hr = (lane >> 3) & 7u;   // (d / 8) & 7 of this lane's row
         for (uint32_t c = 0; c <= nchunk; c++) {
             if (c >= 1) {
-                const float *row = L.hb + ((c - 1) & 1u) * kChunk * kChunkPad + lane * kChunkPad;
-                lds_chain4<4>(reinterpret_cast<const float4 *>(row), kChunk / 4, [&](const float4 &t) {
-                    acc = acc + t.x;
-                    acc = acc + t.y;
-                    acc = acc + t.z;
-                    acc = acc + t.w;
-                });
+                const float4 *r4 = reinterpret_cast<const float4 *>(L.hb + ((c - 1) & 1u) * kChunk * kChunkPad +
+                                                                    lane * kChunkPad);
+                const float4 *e4 = reinterpret_cast<const float4 *>(L.sc + (c - 1) * kChunk);
+#pragma unroll
+                for (int h2 = 0; h2 < 2; h2++) {
+                    float4 pr[8], ew[8];
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        pr[q] = r4[(8 * h2 + q) ^ hr];
+                        ew[q] = e4[8 * h2 + q];
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        acc = acc + pr[q].x;
+                        sum += ew[q].x;
+                        acc = acc + pr[q].y;
+                        sum += ew[q].y;
+                        acc = acc + pr[q].z;
+                        sum += ew[q].z;
+                        acc = acc + pr[q].w;
+                        sum += ew[q].w;
+                    }
+                }
             }
             lds_barrier();
         }
     }
-    if (wave == MW - 1 && lane == 0) misc[8] = sum;
+    if (wave == 0 && lane == 0) misc[8] = sum;
     lds_barrier();
     trace_detail(a, r, 5);
     if (wave == 0) {
