@@ -675,14 +675,35 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     // the row pitch and the group permutation keep both the producers' single
     // float stores (16 dimensions of one position per 16 lanes) and the
     // adder's float4 reads (one row per lane) on distinct banks.
+    // The weights of a chunk are read ahead of the products, so the reads overlap.
+    // e_p == 0 skips the position (f32_axpy), which only matters for a
+    // non-finite v: a chunk with no zero weight, away from the current
+    // position, takes the plain products (the vote is uniform per wavefront).
+    const uint32_t cpos = (uint32_t)pos / kChunk;
     auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
-        float *buf = L.hb + (c & 1u) * kChunk * kChunkPad;
+        float *buf = L.hb + (c & 1u) * kChunk * kChunkPad + d0 * kChunkPad;
         const uint32_t hq = (lane & 15u) >> 1;   // (d / 8) & 7 for d = d0 .. d0 + 3
         float e[GPW];
+        bool anyz = false;
 #pragma unroll
-        for (int i = 0; i < GPW; i++) {   // all weights first, so their reads overlap
+        for (int i = 0; i < GPW; i++) {
             const uint32_t g = (wave - 1) + (MW - 1) * i;
             e[i] = L.sc[c * kChunk + min(4 * g + sub, kChunk - 1)];
+            anyz |= e[i] == 0.0f;
+        }
+        if (!__builtin_amdgcn_readfirstlane(__ballot(anyz) != 0 || c == cpos)) {
+#pragma unroll
+            for (int i = 0; i < GPW; i++) {
+                const uint32_t g = (wave - 1) + (MW - 1) * i;
+                if (g < kChunk / 4) {
+                    const uint32_t col = 4 * (g ^ hq) + sub;
+                    buf[0 * kChunkPad + col] = e[i] * v[i].x;
+                    buf[1 * kChunkPad + col] = e[i] * v[i].y;
+                    buf[2 * kChunkPad + col] = e[i] * v[i].z;
+                    buf[3 * kChunkPad + col] = e[i] * v[i].w;
+                }
+            }
+            return;
         }
 #pragma unroll
         for (int i = 0; i < GPW; i++) {
@@ -691,10 +712,10 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
                 const uint32_t p = c * kChunk + 4 * g + sub, col = 4 * (g ^ hq) + sub;
                 const float4 vv = p == (uint32_t)pos ? vme : v[i];
                 const bool nz = e[i] != 0.0f;
-                buf[(d0 + 0) * kChunkPad + col] = nz ? e[i] * vv.x : 0.0f;
-                buf[(d0 + 1) * kChunkPad + col] = nz ? e[i] * vv.y : 0.0f;
-                buf[(d0 + 2) * kChunkPad + col] = nz ? e[i] * vv.z : 0.0f;
-                buf[(d0 + 3) * kChunkPad + col] = nz ? e[i] * vv.w : 0.0f;
+                buf[0 * kChunkPad + col] = nz ? e[i] * vv.x : 0.0f;
+                buf[1 * kChunkPad + col] = nz ? e[i] * vv.y : 0.0f;
+                buf[2 * kChunkPad + col] = nz ? e[i] * vv.z : 0.0f;
+                buf[3 * kChunkPad + col] = nz ? e[i] * vv.w : 0.0f;
             }
         }
     };
