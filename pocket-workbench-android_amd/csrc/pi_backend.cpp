@@ -464,7 +464,7 @@ int build_mega(pi_ctx *c, Engine &e) {
     e.mega_lds = pi_mega_lds_bytes(e.n_embd, e.n_ff, e.n_ctx);
     if (e.mega_lds > (size_t)maxlds) return PI_OK;
     e.mega_blocks = pi_mega_blocks(c->device, e.n_embd, e.n_ff, e.n_ctx);
-    if (e.mega_blocks == 0) return PI_OK;
+    if (e.mega_blocks < 2 * e.n_head) return PI_OK;   // two attention workgroups per head
     const uint64_t per = pi_mega_layer_words(e.n_embd, e.n_ff, qdim, kdim);
     int r;
     if ((r = dalloc(c, &e.mega_words, per * e.n_layer)) || (r = dalloc(c, &e.mega_part, 2ull * e.mega_blocks)) ||

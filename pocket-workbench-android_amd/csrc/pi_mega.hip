@@ -4,7 +4,9 @@
 //
 // Stages of a layer and who runs them:
 //   S1  every workgroup: x -> RMSNorm + Q8 into LDS; Q/K/V tiles    -> q, k, v
-//   S2  one workgroup per head: RoPE, KV write, attention, Q8       -> att
+//   S2  two workgroups per head (one per half of the dimensions; more
+//       score segments at long contexts): RoPE, KV write, attention,
+//       Q8                                                          -> att
 //   S3  every workgroup: att -> LDS; attn_output tiles, x + proj    -> xb
 //   S4  every workgroup: xb -> RMSNorm + Q8; gate/up tile pairs,
 //       SwiGLU                                                       -> h
@@ -41,7 +43,7 @@ constexpr uint32_t MT = 256;           // threads per workgroup
 constexpr uint32_t MW = MT / 64;       // wavefronts per workgroup
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr uint32_t kChunk = 64;        // attention positions per product chunk
-constexpr uint32_t kChunkPad = 88;     // floats per dimension row of a chunk (16-byte aligned)
+constexpr uint32_t kChunkPad = 68;     // floats per dimension row of a chunk (16-byte aligned)
 constexpr uint32_t kRedFloats = 512;   // small LDS scratch
 constexpr uint32_t kStripFloats = MW * 64 * 16;
 
@@ -497,9 +499,12 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
 // 4-lane accumulators; else the scalar loop), max, e_p = exp(s_p - max),
 // sum over p in order, o[d] = sum over p in order of e_p * v_p[d] skipping
 // e_p == 0 (f32_axpy: product rounded, then added), o * (1/sum), Q8 of o.
-// Wavefronts 1-3 form the products of the next chunk of positions while
-// wavefront 0 (lane = dimension) adds the current chunk in order; wavefront
-// 3 also keeps the running sum of e_p.
+// Two workgroups per head (seg 0 and 1) each form o for one half of the
+// dimensions, which is also one Q8 block of the output; at long contexts
+// more workgroups take segments of the scores.  In a chain workgroup,
+// wavefronts 1-3 form the products of the next chunk of positions while
+// wavefront 0 adds the current chunk in order (lane = dimension) and, in its
+// upper lanes, the running sum of e_p.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &L, uint32_t h,
                                            uint32_t seg, uint32_t nseg, uint32_t layer) {
@@ -508,8 +513,11 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     const uint32_t group = a.n_head / a.n_kv, kvh = h / group;
     const int pos = r.pos;
     const uint32_t n = (uint32_t)pos + 1;
-    // positions [p0, p1) of this segment; segment 0 also forms the sums
-    const uint32_t p0 = (uint32_t)((uint64_t)seg * n / nseg), p1 = (uint32_t)((uint64_t)(seg + 1) * n / nseg);
+    // positions [p0, p1) of this workgroup's scores: every position when the
+    // head has a single score segment (both chain workgroups score it all),
+    // else segment seg of nseg
+    const uint32_t p0 = nseg == 1 ? 0u : (uint32_t)((uint64_t)seg * n / nseg);
+    const uint32_t p1 = nseg == 1 ? n : (uint32_t)((uint64_t)(seg + 1) * n / nseg);
     const uint32_t tag = r.epoch * 64u + layer + 1u;
     const uint64_t *yq = cload(&Yp->q), *yk = cload(&Yp->k), *yv = cload(&Yp->v);
     uint64_t *yatt = cload(&Yp->att);
@@ -597,28 +605,33 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         for (int i = 0; i < 16; i++) kr[i] = kn[i];
     }
     vm_drain();
-    constexpr int GPW = (kChunk / 4 + MW - 2) / (MW - 1);   // groups per product wavefront
+    // The value chain of this head is split by dimension: workgroups 0 and 1
+    // of the head each add dimensions 32 * half .. + 31 (half = seg), which is
+    // also the split of the output into its two Q8 blocks.
+    constexpr uint32_t DHH = DH / 2;
+    constexpr int GPW = 3;        // 8 groups of 8 positions per chunk over 3 product wavefronts
     constexpr int kDepth = 4;
+    const uint32_t half = seg;
     const uint32_t nchunk = (n + kChunk - 1) / kChunk;
-    const uint32_t d0 = 4 * (lane % 16), sub = lane / 16;
-    const float4 vme = reinterpret_cast<const float4 *>(vcur)[lane % 16];
+    const uint32_t dl = 4 * (lane & 7u), sub = lane >> 3;   // dimensions dl..dl+3 of the half, position 8g + sub
+    const float4 vme = reinterpret_cast<const float4 *>(vcur + DHH * (half & 1u))[lane & 7u];
     float4 vr[kDepth][GPW];
     auto load_v = [&](uint32_t c, float4 (&v)[GPW]) {
 #pragma unroll
         for (int i = 0; i < GPW; i++) {
             const uint32_t g = (wave - 1) + (MW - 1) * i;
-            const uint32_t p = min(c * kChunk + 4 * g + sub, n - 1);
-            v[i] = gld(reinterpret_cast<const float4 *>(vbase + (uint64_t)p * DH))[lane % 16];
+            const uint32_t p = min(c * kChunk + 8 * g + sub, n - 1);
+            v[i] = gld(reinterpret_cast<const float4 *>(vbase + (uint64_t)p * DH + DHH * half))[lane & 7u];
         }
     };
-    // the chain workgroup requests its first V rows before the softmax
+    // the chain workgroups request their first V rows before the softmax
     // (unconditionally: load_v clamps to row n - 1, and a fixed number of
     // loads per ring slot lets the compiler wait for the oldest slot only)
-    if (seg == 0 && wave != 0) {
+    if (seg < 2 && wave != 0) {
 #pragma unroll
         for (int k = 0; k < kDepth; k++) load_v(k, vr[k]);
     }
-    if (seg == nseg - 1 && tid == ((uint32_t)pos - p0) % MT) {
+    if ((nseg == 1 || seg == nseg - 1) && tid == ((uint32_t)pos - p0) % MT) {
         float4 kc4[16];
 #pragma unroll
         for (int i = 0; i < 16; i++) kc4[i] = reinterpret_cast<const float4 *>(kcur)[i];
@@ -645,15 +658,18 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     }
     for (uint32_t p = p0 + tid; p < p1; p += MT) L.sc[p] = pi_expf(L.sc[p] - mx);
     if (nseg > 1) {
+        // every segment publishes its e_p; the two chain workgroups read the
+        // positions outside their own segment
         uint64_t *ae = a.aexp + (uint64_t)h * a.n_ctx;
-        if (seg != 0) {
-            for (uint32_t p = p0 + tid; p < p1; p += MT) ll_put(ae + p, __float_as_uint(L.sc[p]), tag);
+        for (uint32_t p = p0 + tid; p < p1; p += MT) ll_put(ae + p, __float_as_uint(L.sc[p]), tag);
+        if (seg >= 2) {
             lds_barrier();
             return true;
         }
-        // segment 0 adds over every position: e_p of the other segments
-        const bool oke = wg_poll<8>(ae + p1, n - p1, tag, a.abort_flag,
-                                    [&](uint32_t i, uint32_t bits) { L.sc[p1 + i] = __uint_as_float(bits); });
+        bool oke = wg_poll<8>(ae, p0, tag, a.abort_flag, [&](uint32_t i, uint32_t bits) { L.sc[i] = __uint_as_float(bits); });
+        if (oke)
+            oke = wg_poll<8>(ae + p1, n - p1, tag, a.abort_flag,
+                             [&](uint32_t i, uint32_t bits) { L.sc[p1 + i] = __uint_as_float(bits); });
         PI_POLL_OR_LEAVE(oke);
     }
     // e_p = 0 past the last position up to the end of its chunk, so every
@@ -663,40 +679,37 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     lds_barrier();
     trace_detail(a, r, 4);
 
-    // Products e_p * v_p[d] of chunk c go to buffer c & 1, laid out [d][p].
-    // A chunk is 16 groups of 4 positions; wavefronts 1-3 own groups w-1,
-    // w+2, ... (lane l: position 4g + l/16, dimensions 4(l%16)..+3, one
-    // 16-byte load) and keep the V rows of the next kDepth chunks in flight
-    // in registers; wavefront 0 adds chunk c - 1 in order while chunk c is
-    // being formed.  V rows always come from HBM (rows past the end re-read
-    // row n-1, whose product is 0 since e_p = 0 there); the current
-    // position's row is taken from LDS.
-    // Product (d, p) of a chunk is at row d, float4 group (p / 4) ^ ((d / 8) & 7):
-    // the row pitch and the group permutation keep both the producers' single
-    // float stores (16 dimensions of one position per 16 lanes) and the
-    // adder's float4 reads (one row per lane) on distinct banks.
-    // The weights of a chunk are read ahead of the products, so the reads overlap.
-    // e_p == 0 skips the position (f32_axpy), which only matters for a
-    // non-finite v: a chunk with no zero weight, away from the current
-    // position, takes the plain products (the vote is uniform per wavefront).
+    // Products e_p * v_p[d] of chunk c go to buffer c & 1: row d of the half
+    // (32 rows), float4 group (p / 4) ^ ((d / 8) & 3), row pitch kChunkPad.
+    // The pitch and the group permutation keep the producers' single-float
+    // stores (4 dimensions x 8 positions per 32 lanes) and the adder's float4
+    // reads (one row per lane) on distinct banks.  Wavefronts 1-3 own groups
+    // w-1, w+2, ... of 8 positions (lane l: position 8g + l/8, dimensions
+    // dl..dl+3, one 16-byte load) and keep the V rows of the next kDepth
+    // chunks in flight in registers.  V rows always come from HBM (rows past
+    // the end re-read row n-1, whose product is 0 since e_p = 0 there); the
+    // current position's row is taken from LDS.  e_p == 0 skips the position
+    // (f32_axpy), which only matters for a non-finite v: a chunk with no zero
+    // weight, away from the current position, takes the plain products (the
+    // vote is uniform per wavefront).
     const uint32_t cpos = (uint32_t)pos / kChunk;
     auto store_products = [&](uint32_t c, const float4 (&v)[GPW]) {
-        float *buf = L.hb + (c & 1u) * kChunk * kChunkPad + d0 * kChunkPad;
-        const uint32_t hq = (lane & 15u) >> 1;   // (d / 8) & 7 for d = d0 .. d0 + 3
+        float *buf = L.hb + (c & 1u) * DHH * kChunkPad + dl * kChunkPad;
+        const uint32_t hq = (lane & 7u) >> 1;   // (d / 8) & 3 for d = dl .. dl + 3
         float e[GPW];
         bool anyz = false;
 #pragma unroll
-        for (int i = 0; i < GPW; i++) {
+        for (int i = 0; i < GPW; i++) {   // all weights first, so their reads overlap
             const uint32_t g = (wave - 1) + (MW - 1) * i;
-            e[i] = L.sc[c * kChunk + min(4 * g + sub, kChunk - 1)];
+            e[i] = L.sc[c * kChunk + min(8 * g + sub, kChunk - 1)];
             anyz |= e[i] == 0.0f;
         }
         if (!__builtin_amdgcn_readfirstlane(__ballot(anyz) != 0 || c == cpos)) {
 #pragma unroll
             for (int i = 0; i < GPW; i++) {
                 const uint32_t g = (wave - 1) + (MW - 1) * i;
-                if (g < kChunk / 4) {
-                    const uint32_t col = 4 * (g ^ hq) + sub;
+                if (g < kChunk / 8) {
+                    const uint32_t col = 4 * ((2 * g + (sub >> 2)) ^ hq) + (sub & 3u);
                     buf[0 * kChunkPad + col] = e[i] * v[i].x;
                     buf[1 * kChunkPad + col] = e[i] * v[i].y;
                     buf[2 * kChunkPad + col] = e[i] * v[i].z;
@@ -708,8 +721,9 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
 #pragma unroll
         for (int i = 0; i < GPW; i++) {
             const uint32_t g = (wave - 1) + (MW - 1) * i;
-            if (g < kChunk / 4) {
-                const uint32_t p = c * kChunk + 4 * g + sub, col = 4 * (g ^ hq) + sub;
+            if (g < kChunk / 8) {
+                const uint32_t p = c * kChunk + 8 * g + sub;
+                const uint32_t col = 4 * ((2 * g + (sub >> 2)) ^ hq) + (sub & 3u);
                 const float4 vv = p == (uint32_t)pos ? vme : v[i];
                 const bool nz = e[i] != 0.0f;
                 buf[0 * kChunkPad + col] = nz ? e[i] * vv.x : 0.0f;
@@ -719,17 +733,17 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
             }
         }
     };
-    float acc = 0.0f, sum = 0.0f;
     // Step c (0..nchunk): wavefronts 1-3 store the products of chunk c and
     // refill the ring slot they used with the rows of chunk c + kDepth;
-    // wavefront 0 adds chunk c - 1 (lane = dimension) and, in every lane, the
-    // weights of that chunk into the sum of e_p (two independent chains).
-    // Producers and adder run separate loops with the same barrier count.  In
-    // the producers' main loop every step of a group issues the same loads
-    // (rows past the end re-read row n - 1), so each ring slot keeps its own
-    // registers and a wavefront waits only for its oldest slot while the
-    // others stay in flight; the last steps, whose rows are already
+    // wavefront 0 adds chunk c - 1: lanes 0-31 their dimension's products,
+    // lanes 32-63 the weights (the sum of e_p, the same in each of them), so
+    // one add per position covers both chains.  Producers and adder run
+    // separate loops with the same barrier count.  In the producers' main
+    // loop every step of a group issues the same loads, so each ring slot
+    // keeps its own registers and a wavefront waits only for its oldest slot
+    // while the others stay in flight; the last steps, whose rows are already
     // requested, run without refills.
+    float acc = 0.0f;
     if (wave != 0) {
         uint32_t c0 = 0;
         for (; c0 + kDepth <= nchunk; c0 += kDepth) {
@@ -749,54 +763,46 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
             lds_barrier();
         }
     } else {
-        const uint32_t hr = (lane >> 3) & 7u;   // (d / 8) & 7 of this lane's row
+        const bool wlane = lane >= DHH;                          // weight lanes
+        const uint32_t hr = wlane ? 0u : (lane >> 3) & 3u;       // (d / 8) & 3 of this lane's row
         for (uint32_t c = 0; c <= nchunk; c++) {
             if (c >= 1) {
-                const float4 *r4 = reinterpret_cast<const float4 *>(L.hb + ((c - 1) & 1u) * kChunk * kChunkPad +
-                                                                    lane * kChunkPad);
-                const float4 *e4 = reinterpret_cast<const float4 *>(L.sc + (c - 1) * kChunk);
+                const float4 *src = wlane ? reinterpret_cast<const float4 *>(L.sc + (c - 1) * kChunk)
+                                          : reinterpret_cast<const float4 *>(L.hb + ((c - 1) & 1u) * DHH * kChunkPad +
+                                                                             lane * kChunkPad);
 #pragma unroll
                 for (int h2 = 0; h2 < 2; h2++) {
-                    float4 pr[8], ew[8];
+                    float4 t[8];
+#pragma unroll
+                    for (int q = 0; q < 8; q++) t[q] = src[(8 * h2 + q) ^ hr];
 #pragma unroll
                     for (int q = 0; q < 8; q++) {
-                        pr[q] = r4[(8 * h2 + q) ^ hr];
-                        ew[q] = e4[8 * h2 + q];
-                    }
-#pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        acc = acc + pr[q].x;
-                        sum += ew[q].x;
-                        acc = acc + pr[q].y;
-                        sum += ew[q].y;
-                        acc = acc + pr[q].z;
-                        sum += ew[q].z;
-                        acc = acc + pr[q].w;
-                        sum += ew[q].w;
+                        acc = acc + t[q].x;
+                        acc = acc + t[q].y;
+                        acc = acc + t[q].z;
+                        acc = acc + t[q].w;
                     }
                 }
             }
             lds_barrier();
         }
     }
-    if (wave == 0 && lane == 0) misc[8] = sum;
-    lds_barrier();
     trace_detail(a, r, 5);
     if (wave == 0) {
-        const float tot = misc[8];
+        const float tot = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), DHH));   // sum of e_p
         const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-        const float o = acc * inv;
-        int8_t *qst = reinterpret_cast<int8_t *>(misc + 16);     // 64 quants
-        float *dst = misc + 32;                                  // 2 scales
-        int32_t *sst = reinterpret_cast<int32_t *>(misc + 34);   // 2 sums
-        q8_block32(o, (int)(lane % 32), qst + (lane / 32) * 32, dst + lane / 32, sst + lane / 32, true);
+        const float o = acc * inv;                               // lanes 0-31: this half's outputs
+        float dd;
+        int bs;
+        const int iv = q8_block32_core(o, dd, bs);               // lanes 32-63 form a block that is not used
+        int8_t *qst = reinterpret_cast<int8_t *>(misc + 16);     // 32 quants
+        if (lane < DHH) qst[lane] = (int8_t)iv;
         wave_sync();
-        // att words: quants (16 per head), then qdim/32 scales, then qdim/32 sums
+        // att words: quants (16 per head, 8 per half), then qdim/32 scales, then qdim/32 sums
         const uint32_t qdim = a.n_head * DH;
-        if (lane < 16) ll_put(yatt + h * 16 + lane, reinterpret_cast<const uint32_t *>(qst)[lane], r.epoch);
-        else if (lane < 18) ll_put(yatt + qdim / 4 + h * 2 + (lane - 16), __float_as_uint(dst[lane - 16]), r.epoch);
-        else if (lane < 20)
-            ll_put(yatt + qdim / 4 + qdim / 32 + h * 2 + (lane - 18), (uint32_t)sst[lane - 18], r.epoch);
+        if (lane < 8) ll_put(yatt + h * 16 + half * 8 + lane, reinterpret_cast<const uint32_t *>(qst)[lane], r.epoch);
+        else if (lane == 8) ll_put(yatt + qdim / 4 + h * 2 + half, __float_as_uint(dd), r.epoch);
+        else if (lane == 9) ll_put(yatt + qdim / 4 + qdim / 32 + h * 2 + half, (uint32_t)bs, r.epoch);
     }
     lds_barrier();
     return true;
@@ -1092,7 +1098,8 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
             uint32_t nseg = (n + PI_MEGA_SEG_LEN - 1) / PI_MEGA_SEG_LEN;
             nseg = min(nseg, min(PI_MEGA_MAX_SEG, nb / a.n_head));
             nseg = max(nseg, 1u);
-            for (uint32_t j = nb - 1 - blockIdx.x; j < a.n_head * nseg; j += nb)
+            const uint32_t nwg = max(nseg, 2u);   // at least the two chain workgroups
+            for (uint32_t j = nb - 1 - blockIdx.x; j < a.n_head * nwg; j += nb)
                 if (!stage_attn(a, r, Y, L, j % a.n_head, j / a.n_head, nseg, l)) return;
         }
         trace_mark(a, 3 + 5 * l);
