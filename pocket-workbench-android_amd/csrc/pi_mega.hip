@@ -348,7 +348,7 @@ __device__ __forceinline__ bool poll_x(const Lds &L, const uint64_t *src, uint32
 // keeps the values in registers instead of re-reading the descriptor (a
 // serial chain of scalar-cache misses) after the wait.
 struct Geo {
-    uint32_t nt, upr, ul;
+    uint32_t nt, upr, ul, rpw;
 };
 // A uniform value read from a descriptor, held in registers from here on (see
 // Geo).
@@ -357,9 +357,9 @@ template <typename V> __device__ __forceinline__ V keep(V v) {
     return v;
 }
 template <typename SS> __device__ __forceinline__ Geo geo_of(const SS &S) {
-    Geo g{ms_total(S), ms_upr(S), 0u};
+    Geo g{ms_total(S), ms_upr(S), 0u, ms_rpw(S)};
     g.ul = (threadIdx.x & 63u) % g.upr;
-    asm volatile("" : "+s"(g.nt), "+s"(g.upr), "+v"(g.ul));
+    asm volatile("" : "+s"(g.nt), "+s"(g.upr), "+v"(g.ul), "+s"(g.rpw));
     return g;
 }
 
@@ -398,6 +398,38 @@ __device__ __forceinline__ void gemv_ring(const SS &S, const Geo &g, const Lds &
             gt += stride;
         }
     }
+}
+
+// One-row tiles (rows longer than 63 units) of a single matrix whose tiles of
+// this wavefront are all in the ring (first + P * stride >= total): the terms
+// of every tile go to the strip first, then lanes 0..P-1 add their own row's
+// terms at once, so the in-order row chains overlap instead of following one
+// another.  Row of ring slot k = first + k * stride.
+template <uint32_t T, int G, int P, typename SS, typename Out>
+__device__ __forceinline__ void gemv_ring_rows1(const Geo &g, const Lds &L, const Unit<T, G> (&U)[P],
+                                                const TileRef (&R)[P], uint32_t first, uint32_t stride, Out out) {
+    constexpr int TPU = QT<T>::TPB * G;
+    const uint32_t lane = threadIdx.x & 63u, per_row = g.upr * TPU;
+    if (first >= g.nt) return;
+    Slice<T, G> SL;
+    SL.load_swz(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+    uint32_t ntile = 0;
+#pragma unroll
+    for (int k = 0; k < P; k++) {
+        if (first + (uint32_t)k * stride < g.nt) {
+            float term[TPU];
+            int isum[TPU];
+            unit_terms<T, G>(U[k], SL, term, isum);
+            if (lane < R[k].lanes) {
+#pragma unroll
+                for (int t = 0; t < TPU; t++) L.strip[k * per_row + lane * TPU + t] = term[t];
+            }
+            ntile = (uint32_t)k + 1;
+        }
+    }
+    wave_sync();
+    if (lane < ntile) out(0u, first + lane * stride, 0.0f + chain_sum(L.strip + lane * per_row, per_row));
+    wave_sync();
 }
 
 // Calls f(integral_constant<T>, integral_constant<G>) for the runtime type/g.
@@ -449,7 +481,7 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
     const float *attn_norm = cload(&Yp->attn_norm);
     uint64_t *oq = keep(cload(&Yp->q)), *okk = keep(cload(&Yp->k)), *ov = keep(cload(&Yp->v));
     const Geo gA = geo_of(SA);
-    const Geo gB = ms_n(SB) ? geo_of(SB) : Geo{0u, 1u, 0u};
+    const Geo gB = ms_n(SB) ? geo_of(SB) : Geo{0u, 1u, 0u, 1u};
     const uint32_t ntA = gA.nt, ntB = gB.nt;
     // segment B continues the wavefront numbering after segment A
     const uint32_t firstB = (gw + nw - ntA % nw) % nw;
@@ -962,6 +994,15 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxo + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
         };
+        if constexpr (T == PI_TYPE_Q4_0 || T == PI_TYPE_Q8_0) {
+            constexpr uint32_t TPU = QT<T>::TPB * G;
+            // every tile of this wavefront in the ring, and three rows of terms
+            // (plus the chain reader's read-ahead) inside its strip
+            if (g.rpw == 1 && ms_n(SD) == 1 && gw + 3 * nw >= g.nt && 3 * g.upr * TPU + kChainPad <= 64u * 16u) {
+                gemv_ring_rows1<T, G, 3, SetRef>(g, L, U, R, gw, nw, out);
+                return;
+            }
+        }
         gemv_ring<T, G, 3>(SD, g, L, U, R, gw, nw, out);
         trace_detail(a, r, 11);
         trace_clock(a, r, 15);
