@@ -495,6 +495,8 @@ int build_mega(pi_ctx *c, Engine &e) {
         Y.g_o = L.o->L.g;
         Y.gu = mset({L.gate, L.up});
         Y.t_gu = L.gate->L.type;
+        Y.h_q8 = same_layout(L.gate, L.up) &&
+                 pi_mega_h_blocks(L.gate->L.type, L.gate->L.upr, e.n_embd, e.n_ff, e.n_ctx);
         Y.down = mset({L.down});
         Y.t_down = L.down->L.type;
         Y.g_down = L.down->L.g;

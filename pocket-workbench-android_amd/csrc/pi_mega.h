@@ -17,14 +17,15 @@ struct pi_mega_layer {
     pig::MatSet o;        // attn_output
     pig::MatSet gu;       // ffn_gate, ffn_up (equal tile counts)
     pig::MatSet down;     // ffn_down
-    uint32_t t_qkv, t_vb, t_o, g_o, t_gu, t_down, g_down, pad_;
+    uint32_t t_qkv, t_vb, t_o, g_o, t_gu, t_down, g_down;
+    uint32_t h_q8;        // 1: h is published as Q8 blocks (pi_mega_h_blocks), else as floats
     const float *attn_norm, *ffn_norm;
     float *kc, *vc;       // this layer's [n_kv][n_ctx][head_dim] caches
     // flag-tagged words written during this layer
     uint64_t *q, *k, *v;  // projections (qdim, kdim, kdim words)
     uint64_t *att;        // Q8 of the attention output: qdim/4 quant words, qdim/32 scales, qdim/32 sums
     uint64_t *xb;         // residual after attn_output (n_embd words)
-    uint64_t *h;          // SwiGLU output (n_ff words)
+    uint64_t *h;          // SwiGLU output: n_ff float words, or with h_q8 n_ff/4 quant words, n_ff/32 scales, n_ff/32 sums
     uint64_t *xo;         // residual after ffn_down (n_embd words)
 };
 
@@ -68,10 +69,15 @@ PI_HD inline uint64_t pi_mega_layer_words(uint32_t ne, uint32_t n_ff, uint32_t q
     return (uint64_t)qdim + 2ull * kdim + (qdim / 4 + qdim / 16) + ne + n_ff + ne;
 }
 // Stage timestamps per workgroup when tracing: start, embedding, 5 per
-// layer, head, then 16 points inside the stages of the middle layer.
-PI_HD inline uint32_t pi_mega_trace_slots(uint32_t n_layer) { return 4 + 5 * n_layer + 16; }
+// layer, head, then 32 points inside the stages of the middle layer.
+PI_HD inline uint32_t pi_mega_trace_slots(uint32_t n_layer) { return 4 + 5 * n_layer + 32; }
 
 size_t pi_mega_lds_bytes(uint32_t ne, uint32_t n_ff, uint32_t n_ctx);
+// Whether the gate/up stage can run workgroups that each own whole Q8 blocks
+// of h (32 rows of gate and of up, eight per wavefront) for gate/up tensors of
+// this type and units per row: every lane holds at most three units of one
+// column, and the four wavefronts' term strips fit the h staging area.
+bool pi_mega_h_blocks(uint32_t type, uint32_t upr, uint32_t ne, uint32_t n_ff, uint32_t n_ctx);
 // Workgroups the launch uses (one per CU when the kernel fits), 0 on error.
 uint32_t pi_mega_blocks(int device, uint32_t ne, uint32_t n_ff, uint32_t n_ctx);
 // neon: batch-1 float orders (else the multi-token chunk orders);

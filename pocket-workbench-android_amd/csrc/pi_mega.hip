@@ -248,9 +248,15 @@ __device__ __forceinline__ void trace_mark(const Cfg &a, uint32_t slot) {
     if (a.trace && threadIdx.x == 0)
         gst(a.trace)[(uint64_t)blockIdx.x * pi_mega_trace_slots(a.n_layer) + slot] = __builtin_amdgcn_s_memrealtime();
 }
-// Point k (< 16) inside a stage of the middle layer.
+// Point k (< 32) inside a stage of the middle layer.
 __device__ __forceinline__ void trace_detail(const Cfg &a, const Run &r, uint32_t k) {
     if (r.detail) trace_mark(a, 3 + 5 * a.n_layer + k);
+}
+// Point k + wave (< 32): recorded by every wavefront of the workgroup.
+__device__ __forceinline__ void trace_detail_w(const Cfg &a, const Run &r, uint32_t k) {
+    if (r.detail && a.trace && (threadIdx.x & 63u) == 0)
+        gst(a.trace)[(uint64_t)blockIdx.x * pi_mega_trace_slots(a.n_layer) + 3 + 5 * a.n_layer + k + (threadIdx.x >> 6)] =
+            __builtin_amdgcn_s_memrealtime();
 }
 // Shader-clock counter at point k of the middle layer (with a real-time point
 // recorded beside it, two of these give the clock the kernel ran at).
@@ -405,9 +411,10 @@ __device__ __forceinline__ void gemv_ring(const SS &S, const Geo &g, const Lds &
 // of every tile go to the strip first, then lanes 0..P-1 add their own row's
 // terms at once, so the in-order row chains overlap instead of following one
 // another.  Row of ring slot k = first + k * stride.
-template <uint32_t T, int G, int P, typename SS, typename Out>
+template <uint32_t T, int G, int P, typename SS, typename Out, typename Mark = NoMark>
 __device__ __forceinline__ void gemv_ring_rows1(const Geo &g, const Lds &L, const Unit<T, G> (&U)[P],
-                                                const TileRef (&R)[P], uint32_t first, uint32_t stride, Out out) {
+                                                const TileRef (&R)[P], uint32_t first, uint32_t stride, Out out,
+                                                Mark mark = Mark{}) {
     constexpr int TPU = QT<T>::TPB * G;
     const uint32_t lane = threadIdx.x & 63u, per_row = g.upr * TPU;
     if (first >= g.nt) return;
@@ -428,8 +435,10 @@ __device__ __forceinline__ void gemv_ring_rows1(const Geo &g, const Lds &L, cons
         }
     }
     wave_sync();
+    mark(21);
     if (lane < ntile) out(0u, first + lane * stride, 0.0f + chain_sum(L.strip + lane * per_row, per_row));
     wave_sync();
+    mark(22);
 }
 
 // Calls f(integral_constant<T>, integral_constant<G>) for the runtime type/g.
@@ -836,14 +845,123 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         else if (lane == 8) ll_put(yatt + qdim / 4 + h * 2 + half, __float_as_uint(dd), r.epoch);
         else if (lane == 9) ll_put(yatt + qdim / 4 + qdim / 32 + h * 2 + half, (uint32_t)bs, r.epoch);
     }
+    trace_detail(a, r, 16);
     lds_barrier();
+    trace_detail(a, r, 17);
     return true;
 }
 
 // ---------------------------------------------------------------------------
+// h blocks of the gate/up stage (S4).
+// ---------------------------------------------------------------------------
+// Block mode (h_q8): the workgroup of block b (h_first_block, then b +
+// gridDim.x, ...) evaluates rows 32b .. 32b + 31 of gate and of up, forms that
+// Q8 block of h and publishes it
+// quantized (Q8Act::prepare, quant_int.rs:17-56): 8 quant words, d and the
+// block sum, so ffn_down reads 10 words per block instead of 32 floats and
+// quantizes nothing.  Wavefront w takes rows 32b + 8w + i (i < 8) of gate
+// (row-dots i) and of up (row-dots 8 + i).  Lane s * upr + j (slot s < rpw)
+// holds unit j of row-dots s, s + rpw, s + 2 rpw, so it keeps the activation
+// slice of one column; lanes past rpw * upr idle.  Each row-dot's terms go to
+// the wavefront's strip in the h staging area, then lanes 0..15 add their
+// row-dot's terms in order at the same time (gate in lanes 0..7, up in 8..15).
+constexpr int kHU = 3;           // units per lane
+constexpr uint32_t kHRowDots = 16;
+
+__host__ __device__ inline uint32_t h_strip_floats(uint32_t upr, uint32_t tpu) {
+    return (kHRowDots * upr * tpu + kChainPad + 3u) & ~3u;
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void h_units(const SetRef &S, const Geo &g, uint32_t n_ff, uint32_t b,
+                                        Unit<T, 1> (&U)[kHU]) {
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t slot = lane / g.upr;
+    const uint32_t ntl = ms_t0(S, 1), lpt = ms_lpt(S);
+    const uint64_t tb = ms_tb(S);
+    const uint8_t *wg = ms_w(S, 0), *wu = ms_w(S, 1);
+#pragma unroll
+    for (int k = 0; k < kHU; k++) {
+        const uint32_t rd = slot + (uint32_t)k * g.rpw;
+        if (slot < g.rpw && rd < kHRowDots) {
+            const uint32_t row = 32u * b + 8u * wave + (rd & 7u);
+            const uint32_t t = row / g.rpw, lr = row - t * g.rpw;
+            const uint32_t lanes = t == ntl - 1 ? (n_ff - t * g.rpw) * g.upr : lpt;
+            U[k].load((rd < 8 ? wg : wu) + (uint64_t)t * tb, lanes, lr * g.upr + g.ul);
+        }
+    }
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void h_block(const Cfg &a, const Run &r, const SetRef &S, const Geo &g, const Lds &L,
+                                        const Slice<T, 1> &SL, const Unit<T, 1> (&U)[kHU], uint32_t b, uint64_t *yh) {
+    constexpr int TPU = QT<T>::TPB;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t slot = lane / g.upr, per_row = g.upr * TPU;
+    float *strip = L.hb + wave * h_strip_floats(g.upr, TPU);
+#pragma unroll
+    for (int k = 0; k < kHU; k++) {
+        const uint32_t rd = slot + (uint32_t)k * g.rpw;
+        if (slot < g.rpw && rd < kHRowDots) {
+            float term[TPU];
+            int isum[TPU];
+            unit_terms<T, 1>(U[k], SL, term, isum);
+#pragma unroll
+            for (int t = 0; t < TPU; t++) strip[rd * per_row + g.ul * TPU + t] = term[t];
+        }
+    }
+    wave_sync();
+    trace_detail(a, r, 24);
+    float v = 0.0f;
+    if (lane < kHRowDots) v = 0.0f + chain_sum(strip + lane * per_row, per_row);
+    const float u = dpp<0x128>(v);   // row_ror:8: lane i < 8 receives up row-dot i from lane i + 8
+    float *hv = L.red + 32;          // h of rows 32b .. 32b + 31
+    if (lane < 8) {
+        const float sg = v / (1.0f + pi_expf(-v));
+        hv[8 * wave + lane] = sg * u;
+    }
+    trace_detail(a, r, 25);
+    lds_barrier();
+    trace_detail(a, r, 26);
+    if (wave == 0) {
+        float dd;
+        int bs;
+        const int iv = q8_block32_core(lane < 32 ? hv[lane] : 0.0f, dd, bs);   // lanes 32-63: a block not used
+        int8_t *qst = reinterpret_cast<int8_t *>(L.red + 64);
+        if (lane < 32) qst[lane] = (int8_t)iv;
+        wave_sync();
+        const uint32_t nq = a.n_ff / 4;
+        if (lane < 8) ll_put(yh + 8 * b + lane, reinterpret_cast<const uint32_t *>(qst)[lane], r.epoch);
+        else if (lane == 8) ll_put(yh + nq + b, __float_as_uint(dd), r.epoch);
+        else if (lane == 9) ll_put(yh + nq + a.n_ff / 32 + b, (uint32_t)bs, r.epoch);
+    }
+    trace_detail(a, r, 27);
+    lds_barrier();   // hv, the quants and the strips are free for the next block
+}
+
+// The block mode's gate/up units of this workgroup's first block (Q4_K).
+using HUnits = Unit<PI_TYPE_Q4_K, 1>[kHU];
+// Marks the units' previous contents as dead (no instruction): without it the
+// conditional loads below would keep the last layer's units live around the
+// whole layer loop.
+__device__ __forceinline__ void h_units_fresh(HUnits &U) {
+#pragma unroll
+    for (int k = 0; k < kHU; k++)
+#pragma unroll
+        for (int j = 0; j < Unit<PI_TYPE_Q4_K, 1>::QC; j++)
+            asm volatile("" : "=v"(U[k].c[j].x), "=v"(U[k].c[j].y), "=v"(U[k].c[j].z), "=v"(U[k].c[j].w));
+}
+// First h block of this workgroup: blocks are numbered from the last
+// workgroup down, away from the first workgroups, which hold the attn_output
+// tiles.
+__device__ __forceinline__ uint32_t h_first_block() { return gridDim.x - 1 - blockIdx.x; }
+
+// ---------------------------------------------------------------------------
 // S3: attn_output on the attention's Q8, x + proj -> xb (model.rs:1091-1097).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw) {
+// HU / hpre: see stage_ffn_up.
+__device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw,
+                                        HUnits &HU, bool &hpre) {
     Lds L = Lc;
     const uint32_t qdim = a.n_head * 64;
     set_act_k(L, qdim);
@@ -858,17 +976,29 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
         Unit<T, G> U[1];
         TileRef R[1];
         const Geo g = geo_of(SO);
+        if (blockIdx.x * MW >= g.nt) return;   // no tile in this workgroup: nothing to wait for
         prefetch_ring<T, G, 1>(SO, g, gw, nw, U, R);
+        if constexpr (T == PI_TYPE_Q4_K) {   // (the other types leave too few registers)
+            if (cload(&Yp->h_q8) && h_first_block() < a.n_ff / 32) {
+                // this workgroup also evaluates an h block: its gate/up units
+                // are requested now, long before the residual they need arrives
+                const SetRef SGU{&Yp->gu};
+                h_units<PI_TYPE_Q4_K>(SGU, geo_of(SGU), a.n_ff, h_first_block(), HU);
+                hpre = true;
+            }
+        }
         lds_barrier();
         const uint32_t nwords = qdim / 4 + qdim / 16, nq = qdim / 4;
         ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag, [&](uint32_t i, uint32_t bits) {
             L.act.qw[i < nq ? 4 * act_chunk(i >> 2) + (i & 3u) : i] = bits;
         });
         if (wg_any(!ok, L.vote)) { ok = false; return; }
+        trace_detail(a, r, 18);
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxb + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
         };
         gemv_ring<T, G, 1>(SO, g, L, U, R, gw, nw, out);
+        trace_detail(a, r, 19);
     });
     if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
     return ok;
@@ -878,7 +1008,10 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
 // S4: RMSNorm + Q8 of xb, gate/up tile pairs, h = silu(gate) * up
 // (model.rs:1099-1115).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw) {
+// hpre: the units of the first block were requested during the attn_output
+// stage (workgroups that also hold an attn_output tile).
+__device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw,
+                                             uint32_t nw, HUnits &HU, bool hpre) {
     Lds L = Lc;
     set_act_k(L, a.ne);
     bool ok = true;
@@ -887,6 +1020,29 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
     const float *ffn_norm = cload(&Yp->ffn_norm);
     const uint64_t *yxb = cload(&Yp->xb);
     uint64_t *yh = keep(cload(&Yp->h));
+    if (cload(&Yp->h_q8)) {
+        constexpr uint32_t T = PI_TYPE_Q4_K;
+        const Geo g = geo_of(SGU);
+        const uint32_t nblk = a.n_ff / 32, nb = gridDim.x, b0 = h_first_block();
+        if (b0 < nblk && !hpre) h_units<T>(SGU, g, a.n_ff, b0, HU);
+        float4 wr[4];
+        load_norm_w(ffn_norm, a.ne, wr);
+        lds_barrier();
+        ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
+        PI_POLL_OR_LEAVE(ok);
+        trace_detail(a, r, 6);
+        norm_q8(L, a.ne, a.eps, wr, r.neon);
+        trace_detail(a, r, 7);
+        if (b0 >= nblk) return true;
+        Slice<T, 1> SL;
+        SL.load_swz(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+        for (uint32_t b = b0; b < nblk; b += nb) {
+            if (b != b0) h_units<T>(SGU, g, a.n_ff, b, HU);
+            h_block<T>(a, r, SGU, g, L, SL, HU, b, yh);
+        }
+        trace_detail(a, r, 8);
+        return true;
+    }
     with_kq(t_gu, [&](auto T_, auto) {
         constexpr uint32_t T = decltype(T_)::value;
         constexpr int TPU = QT<T>::TPB;
@@ -933,6 +1089,7 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
             float g = 0.0f;
             if (lane < Rg.nrows) g = 0.0f + chain_sum(L.strip + lane * per_row, per_row);
             wave_sync();
+            trace_detail(a, r, 20);
             unit_terms<T, 1>(Uu, SL, term, isum);
             if (lane < Ru.lanes) {
 #pragma unroll
@@ -962,6 +1119,7 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
     const SetRef SD{&Yp->down};
     const uint32_t t_down = cload(&Yp->t_down), g_down = cload(&Yp->g_down);
     const uint64_t *yh = cload(&Yp->h);
+    const uint32_t hq8 = cload(&Yp->h_q8);
     uint64_t *yxo = keep(cload(&Yp->xo));
     with_any(t_down, g_down, [&](auto T_, auto G_) {
         constexpr uint32_t T = decltype(T_)::value;
@@ -971,6 +1129,15 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
         const Geo g = geo_of(SD);
         prefetch_ring<T, G, 3>(SD, g, gw, nw, U, R);
         lds_barrier();
+        if (hq8) {
+            // Q8 blocks of h as the gate/up stage published them
+            const uint32_t nq = a.n_ff / 4;
+            ok = wg_poll<8>(yh, nq + a.n_ff / 16, r.epoch, a.abort_flag, [&](uint32_t i, uint32_t bits) {
+                L.act.qw[i < nq ? 4 * act_chunk(i >> 2) + (i & 3u) : i] = bits;
+            });
+            if (wg_any(!ok, L.vote)) { ok = false; return; }
+            trace_detail(a, r, 9);
+        } else {
         ok = wg_poll<23>(yh, a.n_ff, r.epoch, a.abort_flag,
                          [&](uint32_t i, uint32_t bits) { L.hb[i] = __uint_as_float(bits); });
         if (wg_any(!ok, L.vote)) { ok = false; return; }
@@ -990,6 +1157,7 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
             q8_pair(v, h, L.act.qw + 4 * act_chunk(2 * b + h), L.act.d + b, L.act.s + b);
         }
         lds_barrier();
+        }
         trace_detail(a, r, 10);
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxo + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
@@ -999,7 +1167,9 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
             // every tile of this wavefront in the ring, and three rows of terms
             // (plus the chain reader's read-ahead) inside its strip
             if (g.rpw == 1 && ms_n(SD) == 1 && gw + 3 * nw >= g.nt && 3 * g.upr * TPU + kChainPad <= 64u * 16u) {
-                gemv_ring_rows1<T, G, 3, SetRef>(g, L, U, R, gw, nw, out);
+                gemv_ring_rows1<T, G, 3, SetRef>(g, L, U, R, gw, nw, out, [&](uint32_t k) { trace_detail(a, r, k); });
+                trace_detail(a, r, 23);
+                trace_detail_w(a, r, 28);
                 return;
             }
         }
@@ -1144,9 +1314,12 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
                 if (!stage_attn(a, r, Y, L, j % a.n_head, j / a.n_head, nseg, l)) return;
         }
         trace_mark(a, 3 + 5 * l);
-        if (!stage_o(a, r, Y, L, gw, nw)) return;
+        HUnits HU;
+        h_units_fresh(HU);
+        bool hpre = false;
+        if (!stage_o(a, r, Y, L, gw, nw, HU, hpre)) return;
         trace_mark(a, 4 + 5 * l);
-        if (!stage_ffn_up(a, r, Y, L, gw, nw)) return;
+        if (!stage_ffn_up(a, r, Y, L, gw, nw, HU, hpre)) return;
         trace_mark(a, 5 + 5 * l);
         if (!stage_down(a, r, Y, L, gw, nw)) return;
         trace_mark(a, 6 + 5 * l);
@@ -1161,6 +1334,14 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
 }  // namespace
 
 size_t pi_mega_lds_bytes(uint32_t ne, uint32_t n_ff, uint32_t n_ctx) { return lds_plan(ne, n_ff, n_ctx).total; }
+
+bool pi_mega_h_blocks(uint32_t type, uint32_t upr, uint32_t ne, uint32_t n_ff, uint32_t n_ctx) {
+    if (type != PI_TYPE_Q4_K || upr == 0 || upr > 64 || n_ff % 32) return false;
+    const uint32_t rpw = 64 / upr;
+    if (kHU * rpw < kHRowDots) return false;
+    const LdsPlan p = lds_plan(ne, n_ff, n_ctx);
+    return (uint64_t)MW * h_strip_floats(upr, QT<PI_TYPE_Q4_K>::TPB) * 4u <= p.strips - p.hb;
+}
 
 uint32_t pi_mega_blocks(int device, uint32_t ne, uint32_t n_ff, uint32_t n_ctx) {
     hipDeviceProp_t p;
