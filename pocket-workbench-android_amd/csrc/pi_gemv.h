@@ -46,7 +46,15 @@ template <typename T> __device__ __forceinline__ T cload(const T *p) {
 }
 
 __device__ __forceinline__ int sdot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
-__device__ __forceinline__ float h2f(uint32_t bits) { return pi_f16_to_f32((uint16_t)(bits & 0xFFFFu)); }
+// f16 bits (low half) -> f32 with v_cvt_f32_f16: exact for every finite and
+// infinite value (f16 denormals are kept); a signalling NaN comes back quiet,
+// which no term can tell apart, since every use multiplies it.
+__device__ __forceinline__ float h2f(uint32_t bits) {
+    const unsigned short b = (unsigned short)(bits & 0xFFFFu);
+    _Float16 h;
+    __builtin_memcpy(&h, &b, sizeof h);
+    return (float)h;
+}
 __device__ __forceinline__ int comp(const int4 &v, int i) { return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w)); }
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xFFu; }
 __device__ __forceinline__ void wave_sync() {
@@ -340,7 +348,7 @@ template <uint32_t T, int G> struct Slice {
     static constexpr int NQ8 = BE * G / 32;  // Q8 blocks
     int4 a[AI4];
     float ad[NQ8];
-    int as[NQ8];
+    float as[NQ8];   // block sums, converted once (exact: |sum| <= 4064)
     int asum16[T == PI_TYPE_Q6_K ? 16 : 1];  // Q6_K: 16-element sums, (half, g, s) order
 
     // q, d, s: Q8 activation of a whole row (k quants); u: unit index.
@@ -361,7 +369,7 @@ template <uint32_t T, int G> struct Slice {
 #pragma unroll
         for (int i = 0; i < NQ8; i++) {
             ad[i] = d[u * NQ8 + i];
-            as[i] = s[u * NQ8 + i];
+            as[i] = (float)s[u * NQ8 + i];
         }
         if constexpr (T == PI_TYPE_Q6_K) {
 #pragma unroll
@@ -404,7 +412,7 @@ template <uint32_t T, int G> struct Unit {
 
 // Q4_K block (quant_int.rs:330-371): c[0] = d, dmin, scales; c[1..8] = qs.
 // term[sb] = ((d*da)*s)*isum - ((da*dmin)*m)*asum for sub-blocks sb = 0..7.
-__device__ __forceinline__ void terms_q4k(const int4 *c, const int4 *a, const float *ad, const int *as, float *term,
+__device__ __forceinline__ void terms_q4k(const int4 *c, const int4 *a, const float *ad, const float *as, float *term,
                                           int *isum) {
     const float d = h2f((uint32_t)c[0].x), dmin = h2f((uint32_t)c[0].x >> 16);
     const uint32_t S[3] = {(uint32_t)c[0].y, (uint32_t)c[0].z, (uint32_t)c[0].w};
@@ -423,18 +431,18 @@ __device__ __forceinline__ void terms_q4k(const int4 *c, const int4 *a, const fl
                 isum[2 * g + 1] = sdot4(hi, comp(a[4 * g + 2 + h], m), isum[2 * g + 1]);
             }
         }
+    // get_scale_min_k4 (quant_int.rs:245-252) for the 8 sub-blocks at once,
+    // one 6-bit value per byte: scales 0-3 and mins 0-3 are the low 6 bits of
+    // bytes 0-3 and 4-7; scale / min j >= 4 takes its low 4 bits from byte 8+j-4
+    // (low / high nibble) and its top 2 bits from the top of byte j-4 / j.
+    const uint32_t s03 = S[0] & 0x3F3F3F3Fu, m03 = S[1] & 0x3F3F3F3Fu;
+    const uint32_t s47 = (S[2] & 0x0F0F0F0Fu) | ((S[0] >> 2) & 0x30303030u);
+    const uint32_t m47 = ((S[2] >> 4) & 0x0F0F0F0Fu) | ((S[1] >> 2) & 0x30303030u);
 #pragma unroll
     for (int sb = 0; sb < 8; sb++) {
-        uint32_t s, m;  // get_scale_min_k4 (quant_int.rs:245-252)
-        if (sb < 4) {
-            s = byte_of(S[sb / 4], sb % 4) & 63u;
-            m = byte_of(S[(sb + 4) / 4], (sb + 4) % 4) & 63u;
-        } else {
-            const uint32_t b8 = byte_of(S[(sb + 4) / 4], (sb + 4) % 4);
-            s = (b8 & 0xFu) | ((byte_of(S[(sb - 4) / 4], (sb - 4) % 4) >> 6) << 4);
-            m = (b8 >> 4) | ((byte_of(S[sb / 4], sb % 4) >> 6) << 4);
-        }
-        term[sb] = d * ad[sb] * (float)s * (float)isum[sb] - ad[sb] * dmin * (float)m * (float)as[sb];
+        const float s = (float)byte_of(sb < 4 ? s03 : s47, sb % 4);
+        const float m = (float)byte_of(sb < 4 ? m03 : m47, sb % 4);
+        term[sb] = d * ad[sb] * s * (float)isum[sb] - ad[sb] * dmin * m * as[sb];
     }
 }
 
@@ -481,7 +489,7 @@ __device__ __forceinline__ void terms_q6k(const int4 *c, uint32_t dbits, const i
 
 // Q4_0 block (quant_int.rs:303-328): lo nibbles -> 0..15, hi -> 16..31;
 // term = (d*da)*(isum - 8*asum).
-__device__ __forceinline__ void terms_q40(const int4 &c, uint32_t dbits, const int4 *a, float ad, int as, float *term,
+__device__ __forceinline__ void terms_q40(const int4 &c, uint32_t dbits, const int4 *a, float ad, float as, float *term,
                                           int *isum) {
     int s = 0;
 #pragma unroll
@@ -491,7 +499,7 @@ __device__ __forceinline__ void terms_q40(const int4 &c, uint32_t dbits, const i
         s = sdot4((int)((w >> 4) & 0x0F0F0F0Fu), comp(a[1], m), s);
     }
     *isum = s;
-    *term = h2f(dbits) * ad * ((float)s - 8.0f * (float)as);
+    *term = h2f(dbits) * ad * ((float)s - 8.0f * as);
 }
 
 // Q8_0 block (quant_int.rs:282-301): term = (d*da)*isum.
@@ -662,9 +670,12 @@ __device__ __forceinline__ float chain_sum(const float *p, uint32_t n) {
 // Weights of the next tile are requested before the current tile is used
 // (two named buffers, so both stay in registers).
 // per_row: terms per row (units per row * TPU).
-template <uint32_t T, int G, typename Out>
+struct NoMarkG {
+    __device__ void operator()(uint32_t) const {}
+};
+template <uint32_t T, int G, typename Out, typename Mark = NoMarkG>
 __device__ __forceinline__ void consume_tile_pr(uint32_t per_row, const Slice<T, G> &A, const Unit<T, G> &U,
-                                                const TileRef &R, float *strip, Out &out) {
+                                                const TileRef &R, float *strip, Out &out, Mark mark = Mark{}) {
     constexpr int TPU = QT<T>::TPB * G;
     const uint32_t lane = threadIdx.x & 63u;
     float term[TPU];
@@ -675,8 +686,10 @@ __device__ __forceinline__ void consume_tile_pr(uint32_t per_row, const Slice<T,
         for (int t = 0; t < TPU; t++) strip[lane * TPU + t] = term[t];
     }
     wave_sync();
+    mark(30);
     if (lane < R.nrows) out(R.m, R.row0 + lane, 0.0f + chain_sum(strip + lane * per_row, per_row));
     wave_sync();
+    mark(31);
 }
 
 template <uint32_t T, int G, typename SS, typename Out>

@@ -383,19 +383,20 @@ __device__ __forceinline__ void prefetch_ring(const SS &S, const Geo &g, uint32_
     }
 }
 
-template <uint32_t T, int G, int P, typename SS, typename Out>
+template <uint32_t T, int G, int P, typename SS, typename Out, typename Mark = NoMark>
 __device__ __forceinline__ void gemv_ring(const SS &S, const Geo &g, const Lds &L, Unit<T, G> (&U)[P],
-                                          TileRef (&R)[P], uint32_t first, uint32_t stride, Out out) {
+                                          TileRef (&R)[P], uint32_t first, uint32_t stride, Out out, Mark mark = Mark{}) {
     const uint32_t lane = threadIdx.x & 63u, nt = g.nt, per_row = g.upr * (QT<T>::TPB * G);
     if (first >= nt) return;
     Slice<T, G> SL;
     SL.load_swz(reinterpret_cast<const int8_t *>(L.act.qw), L.act.d, L.act.s, g.ul);
+    mark(29);
     uint32_t gt = first;
     for (;;) {
 #pragma unroll
         for (int k = 0; k < P; k++) {
             if (gt >= nt) return;
-            consume_tile_pr<T, G>(per_row, SL, U[k], R[k], L.strip, out);
+            consume_tile_pr<T, G>(per_row, SL, U[k], R[k], L.strip, out, mark);
             const uint32_t gn = gt + (uint32_t)P * stride;
             if (gn < nt) {
                 R[k] = tile_ref(S, gn);
@@ -997,7 +998,7 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
         auto out = [&](uint32_t, uint32_t row, float v) {
             ll_put(yxb + row, __float_as_uint(xt_at(L, row) + v), r.epoch);
         };
-        gemv_ring<T, G, 1>(SO, g, L, U, R, gw, nw, out);
+        gemv_ring<T, G, 1>(SO, g, L, U, R, gw, nw, out, [&](uint32_t k) { trace_detail(a, r, k); });
         trace_detail(a, r, 19);
     });
     if (!ok && threadIdx.x == 0) raise_abort(a.abort_flag);
@@ -1169,7 +1170,6 @@ __device__ __forceinline__ bool stage_down(const Cfg &a, Run r, const pi_mega_la
             if (g.rpw == 1 && ms_n(SD) == 1 && gw + 3 * nw >= g.nt && 3 * g.upr * TPU + kChainPad <= 64u * 16u) {
                 gemv_ring_rows1<T, G, 3, SetRef>(g, L, U, R, gw, nw, out, [&](uint32_t k) { trace_detail(a, r, k); });
                 trace_detail(a, r, 23);
-                trace_detail_w(a, r, 28);
                 return;
             }
         }

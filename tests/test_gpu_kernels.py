@@ -123,6 +123,39 @@ def test_gemv_matches_oracle(pih, backend, oracle, t, rows, k):
     backend.clear_weight_cache()
 
 
+# f16 scale patterns: subnormals (smallest, largest, negative), signed zeros,
+# infinities, a quiet and a signalling NaN
+SPECIAL_F16 = [0x0001, 0x03FF, 0x8200, 0x0000, 0x8000, 0x7C00, 0xFC00, 0x7E00, 0x7C01]
+# (block bytes, offsets of the f16 scale fields in a block)
+SCALE_FIELDS = {Q4_K: (144, (0, 2)), Q6_K: (210, (208,)), Q4_0: (18, (0,)), Q8_0: (34, (0,))}
+
+
+@pytest.mark.parametrize("t", [Q4_K, Q6_K, Q4_0, Q8_0])
+def test_gemv_special_scales(pih, backend, oracle, t):
+    """Rows whose block scales (d, and dmin for Q4_K) are f16 subnormals, zeros,
+    infinities and NaNs: finite outputs bitwise equal to the oracle's, NaN
+    outputs in the same rows (quant_int.rs decodes scales with the f16 crate)."""
+    bb, offs = SCALE_FIELDS[t]
+    k = 512
+    rows = 2 + len(SPECIAL_F16) * len(offs)
+    w = _rows(pih, t, rows, k, 300 + t).copy()
+    rb = pih.row_bytes(t, k)
+    r = 2
+    for off in offs:
+        for v in SPECIAL_F16:
+            row = w[r * rb:(r + 1) * rb].reshape(-1, bb)
+            row[:, off] = v & 0xFF
+            row[:, off + 1] = v >> 8
+            r += 1
+    x = np.random.default_rng(7).standard_normal(k).astype(np.float32)
+    got = backend.matvec(t, w, k, x, rows)
+    want = oracle.Pool(4).matmul(t, w, rb, k, x, 1, rows, oracle.Act(x, k, 1))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    fin = ~np.isnan(want)
+    assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
+    backend.clear_weight_cache()
+
+
 def test_gemv_config2_head(pih, backend, oracle):
     """Q6_K output head, 122753 x 2304; x ~ N(0,1), RMS-normalised."""
     rows, k = 122753, 2304
