@@ -52,7 +52,7 @@ MODEL_SEED, PROMPT_SEED, N_PROMPT = 1234, 77, 128
 # HBM bytes per Q4_K GEMV launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each
 # scaled by what the counter reads for a 256 MiB copy (read x1.9997, write x1.0):
 # profiles/gemv_q4k_5760x2304_traffic.md
-Q4K_TRAFFIC_BYTES = round((3751.1 * 1.9997 + 45.0 * 1.0) * 1024)
+Q4K_TRAFFIC_BYTES = round((3714.5 * 1.9997 + 25.7 * 1.0) * 1024)
 
 
 def splitmix_ids(seed: int, n: int, vocab: int) -> list:
