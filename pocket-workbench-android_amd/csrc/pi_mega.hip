@@ -510,7 +510,7 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);
             if (wg_any(!ok, L.vote)) { ok = false; return; }
             trace_detail(a, r, 0);
-            trace_clock(a, r, 14);
+            // (clock point 14 used by the attention trace)
             norm_q8(L, a.ne, a.eps, wr, r.neon, [&](uint32_t k) { trace_detail(a, r, k); });
             trace_detail(a, r, 1);
             auto outA = [&](uint32_t m, uint32_t row, float v) {
@@ -567,8 +567,8 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     float *qs = L.red, *kcur = L.red + 64, *vcur = L.red + 128, *misc = L.red + 192;
     float *kbase = ykc + (uint64_t)kvh * a.n_ctx * DH;
     float *vbase = yvc + (uint64_t)kvh * a.n_ctx * DH;
-    // Every K row comes from HBM (the row of the current position may not be
-    // visible yet and is recomputed from LDS below), so loads never share a
+    // Every K row is requested from HBM (the row of the current position may
+    // not be visible yet; the score loop takes it from LDS), so loads never share a
     // destination register with an LDS read.
     auto load_k = [&](uint32_t p, float4 (&kr)[16]) {
         const PI_GLOBAL float4 *src = gld(reinterpret_cast<const float4 *>(kbase + (uint64_t)p * DH));
@@ -600,6 +600,7 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         kcur[2 * i + 1] = y0 * s + y1 * c;
     }
     lds_barrier();
+    trace_detail(a, r, 20);
     if (seg == 0 && h % group == 0 && tid < DH) {
         gst(kbase)[(uint64_t)pos * DH + tid] = kcur[tid];
         gst(vbase)[(uint64_t)pos * DH + tid] = vcur[tid];
@@ -638,14 +639,17 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     for (uint32_t p = p0 + tid; p < p1; p += MT) {
         float4 kn[16];
         if (p + MT < p1) load_k(p + MT, kn);
-        const float s = score(kr);
-        if (p != (uint32_t)pos) {
-            L.sc[p] = s;
-            mx = fmaxf(mx, s);
+        if (p == (uint32_t)pos) {   // this position's row: from LDS
+#pragma unroll
+            for (int i = 0; i < 16; i++) kr[i] = reinterpret_cast<const float4 *>(kcur)[i];
         }
+        const float s = score(kr);
+        L.sc[p] = s;
+        mx = fmaxf(mx, s);
 #pragma unroll
         for (int i = 0; i < 16; i++) kr[i] = kn[i];
     }
+    trace_detail(a, r, 28);
     vm_drain();
     // The value chain of this head is split by dimension: workgroups 0 and 1
     // of the head each add dimensions 32 * half .. + 31 (half = seg), which is
@@ -673,14 +677,7 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
 #pragma unroll
         for (int k = 0; k < kDepth; k++) load_v(k, vr[k]);
     }
-    if ((nseg == 1 || seg == nseg - 1) && tid == ((uint32_t)pos - p0) % MT) {
-        float4 kc4[16];
-#pragma unroll
-        for (int i = 0; i < 16; i++) kc4[i] = reinterpret_cast<const float4 *>(kcur)[i];
-        const float s = score(kc4);
-        L.sc[pos] = s;
-        mx = fmaxf(mx, s);
-    }
+    trace_detail(a, r, 15);
     mx = wave_max(mx);
     if (lane == 0) misc[wave] = mx;
     lds_barrier();
@@ -699,6 +696,7 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
         for (uint32_t i = 0; i < nseg; i++) mx = fmaxf(mx, misc[8 + i]);
     }
     for (uint32_t p = p0 + tid; p < p1; p += MT) L.sc[p] = pi_expf(L.sc[p] - mx);
+    trace_detail(a, r, 14);
     if (nseg > 1) {
         // every segment publishes its e_p; the two chain workgroups read the
         // positions outside their own segment
