@@ -252,12 +252,6 @@ __device__ __forceinline__ void trace_mark(const Cfg &a, uint32_t slot) {
 __device__ __forceinline__ void trace_detail(const Cfg &a, const Run &r, uint32_t k) {
     if (r.detail) trace_mark(a, 3 + 5 * a.n_layer + k);
 }
-// Point k + wave (< 32): recorded by every wavefront of the workgroup.
-__device__ __forceinline__ void trace_detail_w(const Cfg &a, const Run &r, uint32_t k) {
-    if (r.detail && a.trace && (threadIdx.x & 63u) == 0)
-        gst(a.trace)[(uint64_t)blockIdx.x * pi_mega_trace_slots(a.n_layer) + 3 + 5 * a.n_layer + k + (threadIdx.x >> 6)] =
-            __builtin_amdgcn_s_memrealtime();
-}
 // Shader-clock counter at point k of the middle layer (with a real-time point
 // recorded beside it, two of these give the clock the kernel ran at).
 __device__ __forceinline__ void trace_clock(const Cfg &a, const Run &r, uint32_t k) {
