@@ -28,7 +28,7 @@
 // so the HBM latency of the weights overlaps the hand-off.  The GEMV core,
 // Q8 rule and float orders are those of pi_gemv.h / pi_decode.hip, so the
 // results are bit-identical to the CPU path.
-#define PI_CHAIN_B 6   // per-row chains read 6 float4 ahead (the kernel is at its register limit)
+#define PI_CHAIN_B 4   // per-row chains read 4 float4 ahead (the kernel is at its register limit)
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
