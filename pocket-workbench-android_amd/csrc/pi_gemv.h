@@ -398,16 +398,19 @@ template <uint32_t T, int G> struct Unit {
     uint32_t db[ND];
 
     // tb: tile base; lanes: units in this tile; l: this lane's unit (< lanes).
-    __device__ __forceinline__ void load(const uint8_t *tb, uint32_t lanes, uint32_t l) {
+    __device__ __forceinline__ void load(const uint8_t *tb, uint32_t lanes, uint32_t l) { load_part<0, QC>(tb, lanes, l); }
+    // Chunks J0 .. J1-1 only (and the D plane with the last chunk), so a unit
+    // can be requested in two parts.
+    template <int J0, int J1> __device__ __forceinline__ void load_part(const uint8_t *tb, uint32_t lanes, uint32_t l) {
         // Weights are read once per token: non-temporal loads, so they do not
         // evict what is reused from the L2 (code, tagged words, activations).
         typedef int v4i __attribute__((ext_vector_type(4)));
 #pragma unroll
-        for (int j = 0; j < QC; j++) {
+        for (int j = J0; j < J1; j++) {
             const v4i t = __builtin_nontemporal_load(gld(reinterpret_cast<const v4i *>(tb + ((uint64_t)j * lanes + l) * 16u)));
             c[j] = make_int4(t.x, t.y, t.z, t.w);
         }
-        if constexpr (QT<T>::DF) {
+        if constexpr (QT<T>::DF && J1 == QC) {
             const PI_GLOBAL uint16_t *dp = gld(reinterpret_cast<const uint16_t *>(tb + (uint64_t)lanes * QC * 16u));
 #pragma unroll
             for (int b = 0; b < G; b++) db[b] = __builtin_nontemporal_load(dp + (uint64_t)b * lanes + l);

@@ -270,12 +270,14 @@ __device__ __forceinline__ void trace_clock(const Cfg &a, const Run &r, uint32_t
 struct NoMark {
     __device__ void operator()(uint32_t) const {}
 };
-template <typename Mark = NoMark>
+// drain = false: loads issued after the input's wait may still be in flight
+// (the caller's own tile requests); nothing here waits for them.
+template <bool drain = true, typename Mark = NoMark>
 __device__ __forceinline__ void norm_q8(const Lds &L, uint32_t ne, float eps, const float4 (&wr)[4], bool neon,
                                         Mark mark = Mark{}) {
     const uint32_t tid = threadIdx.x;
     const uint32_t n4 = ne / 32;  // float4 per transposed row (a multiple of 4: ne % 128 == 0)
-    vm_drain();
+    if constexpr (drain) vm_drain();
     mark(12);
     if (neon) {
         if (tid < 8) L.red[tid] = sumsq_fma_chain<6>(reinterpret_cast<const float4 *>(L.xt + tid * L.XT), n4);
@@ -496,8 +498,17 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             Unit<TB, 1> UB[1];
             TileRef RA[1], RB[1];
             const bool b_first = gw >= ntA && firstB < ntB;   // B is this wavefront's first work
-            if (b_first) prefetch_ring<TB, 1, 1>(SB, gB, firstB, nw, UB, RB);
-            else prefetch_ring<TA, 1, 1>(SA, gA, gw, nw, UA, RA);
+            // The first tile is requested in two halves: the first before the
+            // wait for the residual, the second once it has arrived (the
+            // wait's loads complete only after every load issued before them,
+            // and the norm that follows takes longer than the second half).
+            const uint32_t lane = threadIdx.x & 63u;
+            constexpr int HA = Unit<TA, 1>::QC / 2, HB = Unit<TB, 1>::QC / 2;
+            const bool has = b_first || gw < ntA;
+            if (b_first) RB[0] = tile_ref(SB, firstB);
+            else if (gw < ntA) RA[0] = tile_ref(SA, gw);
+            if (b_first) UB[0].template load_part<0, HB>(RB[0].base, RB[0].lanes, min(lane, RB[0].lanes - 1));
+            else if (has) UA[0].template load_part<0, HA>(RA[0].base, RA[0].lanes, min(lane, RA[0].lanes - 1));
             float4 wr[4];
             load_norm_w(attn_norm, a.ne, wr);
             lds_barrier();
@@ -505,7 +516,11 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             if (wg_any(!ok, L.vote)) { ok = false; return; }
             trace_detail(a, r, 0);
             // (clock point 14 used by the attention trace)
-            norm_q8(L, a.ne, a.eps, wr, r.neon, [&](uint32_t k) { trace_detail(a, r, k); });
+            if (b_first)
+                UB[0].template load_part<HB, Unit<TB, 1>::QC>(RB[0].base, RB[0].lanes, min(lane, RB[0].lanes - 1));
+            else if (has)
+                UA[0].template load_part<HA, Unit<TA, 1>::QC>(RA[0].base, RA[0].lanes, min(lane, RA[0].lanes - 1));
+            norm_q8<false>(L, a.ne, a.eps, wr, r.neon, [&](uint32_t k) { trace_detail(a, r, k); });
             trace_detail(a, r, 1);
             auto outA = [&](uint32_t m, uint32_t row, float v) {
                 uint64_t *o = m == 0 ? oq : (m == 1 ? okk : ov);
