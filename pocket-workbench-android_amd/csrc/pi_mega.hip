@@ -1036,6 +1036,9 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
         float4 wr[4];
         load_norm_w(ffn_norm, a.ne, wr);
         lds_barrier();
+        // Without an h block the residual is needed only by ffn_down: poll
+        // later, so the workgroups that need it now see less traffic.
+        if (b0 >= nblk) __builtin_amdgcn_s_sleep(64);
         ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
         PI_POLL_OR_LEAVE(ok);
         trace_detail(a, r, 6);
