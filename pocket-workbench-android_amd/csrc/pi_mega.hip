@@ -1018,8 +1018,10 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
 // ---------------------------------------------------------------------------
 // hpre: the units of the first block were requested during the attn_output
 // stage (workgroups that also hold an attn_output tile).
+// early: the workgroup ran neither attention nor an attn_output tile in this
+// layer, so it reaches this stage long before the residual exists.
 __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw,
-                                             uint32_t nw, HUnits &HU, bool hpre) {
+                                             uint32_t nw, HUnits &HU, bool hpre, bool early) {
     Lds L = Lc;
     set_act_k(L, a.ne);
     bool ok = true;
@@ -1036,9 +1038,12 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
         float4 wr[4];
         load_norm_w(ffn_norm, a.ne, wr);
         lds_barrier();
-        // Without an h block the residual is needed only by ffn_down: poll
-        // later, so the workgroups that need it now see less traffic.
+        // Without an h block the residual is needed only by ffn_down, and a
+        // workgroup that skipped attention and attn_output waits the better
+        // part of those two stages: both poll later, so the polls that matter
+        // see less traffic.
         if (b0 >= nblk) __builtin_amdgcn_s_sleep(64);
+        else if (early) __builtin_amdgcn_s_sleep(127);
         ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
         PI_POLL_OR_LEAVE(ok);
         trace_detail(a, r, 6);
@@ -1311,6 +1316,7 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
         const uint64_t *xin = l == 0 ? nullptr : cload(&a.layers[l - 1].xo);
         if (!stage_qkv(a, r, Y, L, xin, gw, nw)) return;
         trace_mark(a, 2 + 5 * l);
+        bool busy = false;   // attention or an attn_output tile in this layer
         {
             // long contexts split each head's positions into nseg segments, one
             // workgroup each (at most one item per workgroup: segments wait for
@@ -1320,16 +1326,18 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
             nseg = min(nseg, min(PI_MEGA_MAX_SEG, nb / a.n_head));
             nseg = max(nseg, 1u);
             const uint32_t nwg = max(nseg, 2u);   // at least the two chain workgroups
+            busy = nb - 1 - blockIdx.x < a.n_head * nwg;
             for (uint32_t j = nb - 1 - blockIdx.x; j < a.n_head * nwg; j += nb)
                 if (!stage_attn(a, r, Y, L, j % a.n_head, j / a.n_head, nseg, l)) return;
         }
+        busy = busy || blockIdx.x * MW < ms_total(SetRef{&Y->o});
         trace_mark(a, 3 + 5 * l);
         HUnits HU;
         h_units_fresh(HU);
         bool hpre = false;
         if (!stage_o(a, r, Y, L, gw, nw, HU, hpre)) return;
         trace_mark(a, 4 + 5 * l);
-        if (!stage_ffn_up(a, r, Y, L, gw, nw, HU, hpre)) return;
+        if (!stage_ffn_up(a, r, Y, L, gw, nw, HU, hpre, !busy)) return;
         trace_mark(a, 5 + 5 * l);
         if (!stage_down(a, r, Y, L, gw, nw)) return;
         trace_mark(a, 6 + 5 * l);
