@@ -967,9 +967,10 @@ __device__ __forceinline__ uint32_t h_first_block() { return gridDim.x - 1 - blo
 // ---------------------------------------------------------------------------
 // S3: attn_output on the attention's Q8, x + proj -> xb (model.rs:1091-1097).
 // ---------------------------------------------------------------------------
-// HU / hpre: see stage_ffn_up.
+// HU / hpre: see stage_ffn_up.  early: the workgroup ran no attention in this
+// layer, so it gets here while attention is still running.
 __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer *Yp, const Lds &Lc, uint32_t gw, uint32_t nw,
-                                        HUnits &HU, bool &hpre) {
+                                        HUnits &HU, bool &hpre, bool early) {
     Lds L = Lc;
     const uint32_t qdim = a.n_head * 64;
     set_act_k(L, qdim);
@@ -996,6 +997,7 @@ __device__ __forceinline__ bool stage_o(const Cfg &a, Run r, const pi_mega_layer
             }
         }
         lds_barrier();
+        if (early) __builtin_amdgcn_s_sleep(127);   // poll later: less traffic for the polls that matter
         const uint32_t nwords = qdim / 4 + qdim / 16, nq = qdim / 4;
         ok = wg_poll<3>(yatt, nwords, r.epoch, a.abort_flag, [&](uint32_t i, uint32_t bits) {
             L.act.qw[i < nq ? 4 * act_chunk(i >> 2) + (i & 3u) : i] = bits;
@@ -1330,12 +1332,13 @@ __global__ __launch_bounds__(MT, 1) void k_mega(const pi_mega_args *__restrict__
             for (uint32_t j = nb - 1 - blockIdx.x; j < a.n_head * nwg; j += nb)
                 if (!stage_attn(a, r, Y, L, j % a.n_head, j / a.n_head, nseg, l)) return;
         }
+        const bool attn = busy;
         busy = busy || blockIdx.x * MW < ms_total(SetRef{&Y->o});
         trace_mark(a, 3 + 5 * l);
         HUnits HU;
         h_units_fresh(HU);
         bool hpre = false;
-        if (!stage_o(a, r, Y, L, gw, nw, HU, hpre)) return;
+        if (!stage_o(a, r, Y, L, gw, nw, HU, hpre, !attn)) return;
         trace_mark(a, 4 + 5 * l);
         if (!stage_ffn_up(a, r, Y, L, gw, nw, HU, hpre, !busy)) return;
         trace_mark(a, 5 + 5 * l);
