@@ -1045,7 +1045,10 @@ __device__ __forceinline__ bool stage_ffn_up(const Cfg &a, Run r, const pi_mega_
         // part of those two stages: both poll later, so the polls that matter
         // see less traffic.
         if (b0 >= nblk) __builtin_amdgcn_s_sleep(64);
-        else if (early) __builtin_amdgcn_s_sleep(127);
+        else if (early) {
+            __builtin_amdgcn_s_sleep(127);
+            __builtin_amdgcn_s_sleep(127);
+        }
         ok = poll_x(L, yxb, a.ne, r.epoch, a.abort_flag);
         PI_POLL_OR_LEAVE(ok);
         trace_detail(a, r, 6);
