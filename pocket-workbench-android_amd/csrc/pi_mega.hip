@@ -509,12 +509,12 @@ __device__ __forceinline__ bool stage_qkv(const Cfg &a, Run r, const pi_mega_lay
             else if (gw < ntA) RA[0] = tile_ref(SA, gw);
             if (b_first) UB[0].template load_part<0, HB>(RB[0].base, RB[0].lanes, min(lane, RB[0].lanes - 1));
             else if (has) UA[0].template load_part<0, HA>(RA[0].base, RA[0].lanes, min(lane, RA[0].lanes - 1));
-            float4 wr[4];
-            load_norm_w(attn_norm, a.ne, wr);
             lds_barrier();
             if (xin) ok = poll_x(L, xin, a.ne, r.epoch, a.abort_flag);
             if (wg_any(!ok, L.vote)) { ok = false; return; }
             trace_detail(a, r, 0);
+            float4 wr[4];   // needed only after the sum of squares: requested after the wait too
+            load_norm_w(attn_norm, a.ne, wr);
             // (clock point 14 used by the attention trace)
             if (b_first)
                 UB[0].template load_part<HB, Unit<TB, 1>::QC>(RB[0].base, RB[0].lanes, min(lane, RB[0].lanes - 1));
