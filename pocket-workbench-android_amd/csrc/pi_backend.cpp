@@ -28,7 +28,11 @@ struct pi_tensor {
 
 namespace {
 
-constexpr uint32_t kGemvMaxBlocks = 2048;  // persistent grid cap of the standalone GEMV (1 wave each)
+// Persistent grid cap of the standalone GEMV, in wavefronts (4 per workgroup):
+// 1024 = one workgroup on each of the 256 CUs.  Measured on the 122753x2304
+// Q6_K head: 40.4 us at 1024 against 44-45 us at 2048, 47 at 1536, 49 at 768;
+// a grid that puts a second workgroup on some CUs leaves the others idle at the end.
+constexpr uint32_t kGemvMaxBlocks = 1024;
 constexpr uint32_t kFusedMaxBlocks = 1024; // persistent grid cap of the fused kernels (4 waves each)
 constexpr uint32_t kMaxBatch = 64;     // model.rs:12
 constexpr uint32_t kDecodeChunk = 16;  // decode steps launched between host checks
