@@ -1,33 +1,41 @@
 #!/usr/bin/env python3
 """Decode benchmark of the MI355X pocketinfer backend (one GPU).
 
-Workload: greedy decode of the synthetic MiniCPM-2B-shaped Q4_K_M model
-(40 layers, hidden 2304, 36x64 MHA, FFN 5760, vocab 122753; Q4_K with a Q6_K
-head, Q6_K attn_v and Q8_0 ffn_down in even layers, Q4_0 ffn_down in odd
-ones; f32 KV), prompt of 128 random ids, 256 greedy tokens at batch 1.
-A step is one decode forward (embedding, 40 layers, head, argmax).
+Workload (one step): the full greedy decode of the synthetic MiniCPM-2B-shaped
+Q4_K_M model (40 layers, hidden 2304, 36x64 MHA, FFN 5760, vocab 122753; Q4_K
+with a Q6_K head, Q6_K attn_v and Q8_0 ffn_down in even layers, Q4_0 ffn_down
+in odd ones; f32 KV): a prompt of 128 random ids, then 256 greedy tokens at
+batch 1 (255 decode forwards).  `--steps K` times K such decodes, `--warmup W`
+runs W untimed ones first; the decode length never changes.
 
 metric: decode tok/s = gen_tokens / gen_ms as the reference defines it
 (model.rs:1297-1350, PerfLog.kt:43): n tokens take n-1 forwards.
 
 Also measured here:
-  roofline  -- the Q4_K GEMV kernel at 5760x2304 (one launch = 7 497 216
-               algorithmic bytes: weights + f32 x + f32 y), timed with HIP events
-               on its stream while rotating 70 weight copies (522 MB, twice the
-               256 MB Infinity Cache) so the reads come from HBM;
-  q6k_head  -- the Q6_K head GEMV at 122753x2304 (232 503 398 B per launch);
-  cpu_baseline -- the CPU oracle's decode tok/s on a bounded sample (32-id
-               prompt, 9 greedy tokens) with every host thread.
+  roofline   -- the persistent decode kernel k_mega (one launch = one decode
+                forward): algorithmic bytes per launch = every weight byte of a
+                token (1 766 384 226 B) + the KV rows attention reads and
+                writes (737 280 B per position, positions 0..p for the
+                forward at position p; mean over the 255 forwards) + one
+                embedding row, over the mean device time of a launch, timed
+                with an event pair around every launch of the timed decodes;
+  gemv_q4k / gemv_q6k -- the standalone GEMVs of configs 1 and 2 with their
+                Q8 pass (the whole pi_hip_gemv_dev job) and without it,
+                rotating weight copies (twice the 256 MB Infinity Cache) so
+                the reads come from HBM;
+  prefill    -- the 2048-token prompt on the batched int8-MFMA prefill
+                kernels (64 chunks of 32), then the prompt extended by 512
+                tokens reusing the 2048 cached positions;
+  long_context -- 64 greedy tokens after 4096 and 16384 positions of N(0,1) KV;
+  cpu_baseline -- the CPU oracle's int8 decode (the reference's aarch64 CPU
+                path restated) of the same model on a bounded sample, at 4
+                threads (the reference default) and at every available core
+                (at most 16, the host share of one GPU), plus the restated f32
+                path the reference runs on x86 (quant.rs:377-476).
 
-  prefill  -- the 2048-token prompt of the same model on the batched int8-MFMA
-               prefill kernels (64 chunks of 32), then the prompt extended by
-               512 tokens reusing the 2048 cached positions;
-  long_context -- decode at 4096 and 16384 positions of N(0,1) KV
-               (737 280 KV bytes per position on top of the weights).
-
-Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --profile-gemv   (GEMV launches and a 256 MiB device
-                                         copy only, for counter runs)
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip SECTIONS]
+       python bench.py --profile-gemv     (GEMV launches and a 256 MiB copy, for counter runs)
+       python bench.py --profile-decode   (one 32-token decode, for counter runs)
 """
 import argparse
 import json
@@ -36,22 +44,25 @@ import sys
 import time
 from pathlib import Path
 
-import numpy as np
-
 REPO = Path(__file__).resolve().parent
 sys.path[:0] = [str(REPO), str(REPO / "pocket-workbench-android_amd")]
 
 import pocketinfer_hip as pih  # noqa: E402
 
+METRIC = "decode tok/s, 2B Q4_K_M synthetic; Q4_K/Q6_K GEMV HBM GB/s (% of peak)"
 HBM_PEAK_GBS = 8000.0
 Q4K_ROWS, Q4K_K = 5760, 2304
 Q4K_LAUNCH_BYTES = Q4K_ROWS * (Q4K_K // 256) * 144 + Q4K_K * 4 + Q4K_ROWS * 4     # 7 497 216
 Q6K_ROWS, Q6K_K = 122753, 2304
 Q6K_LAUNCH_BYTES = Q6K_ROWS * (Q6K_K // 256) * 210 + Q6K_K * 4 + Q6K_ROWS * 4     # 232 503 398
-MODEL_SEED, PROMPT_SEED, N_PROMPT = 1234, 77, 128
-# HBM bytes per Q4_K GEMV launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each
-# scaled by what the counter reads for a 256 MiB copy (read x1.9997, write x1.0):
-# profiles/gemv_q4k_5760x2304_traffic.md
+MODEL_SEED, PROMPT_SEED, N_PROMPT, N_GEN = 1234, 77, 128, 256
+KV_BYTES_PER_POS = 2 * 40 * 36 * 64 * 4                                          # 737 280
+EMBD_ROW_BYTES = Q4K_K // 256 * 144                                               # 1 296
+# HBM bytes per k_mega launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each
+# scaled by what the counter reads for a 256 MiB copy; None until measured
+# (profiles/decode_minicpm2b_k_mega_traffic.md).
+K_MEGA_TRAFFIC_BYTES = None
+# Same for the Q4_K GEMV launch (profiles/gemv_q4k_5760x2304_traffic.md).
 Q4K_TRAFFIC_BYTES = round((3714.5 * 1.9997 + 25.7 * 1.0) * 1024)
 
 
@@ -72,17 +83,30 @@ def log(msg):
 
 
 def time_gemv(b, t, rows, k, gen, copies, iters):
+    """(us of the whole job: Q8 of x + GEMV, us of the GEMV alone)."""
     w = gen(1, rows, k)
     ws = [b.upload(t, w, rows, k) for _ in range(copies)]
     x = pih.synth_normal(2, k)
     xd, yd = b.to_device(x), b.alloc(rows * 4)
     qd, dd, sd = b.alloc(k), b.alloc(k // 32 * 4), b.alloc(k // 32 * 4)
     b.q8_quantize_dev(xd.ptr, k, 1, qd.ptr, dd.ptr, sd.ptr)
-    b.time_gemv(ws, qd.ptr, dd.ptr, sd.ptr, yd.ptr, max(copies, 8))          # warm
-    us = b.time_gemv(ws, qd.ptr, dd.ptr, sd.ptr, yd.ptr, iters)
+    b.time_gemv_x(ws, xd.ptr, yd.ptr, max(copies, 8))                       # warm
+    whole = b.time_gemv_x(ws, xd.ptr, yd.ptr, iters)
+    alone = b.time_gemv(ws, qd.ptr, dd.ptr, sd.ptr, yd.ptr, iters)
     for wt in ws:
         wt.free()
-    return us
+    for buf in (xd, yd, qd, dd, sd):
+        buf.free()
+    return whole, alone
+
+
+def gemv_entry(whole_us, alone_us, nbytes, kernel):
+    g = nbytes / (whole_us * 1e-6) / 1e9
+    ga = nbytes / (alone_us * 1e-6) / 1e9
+    return {"kernel": kernel, "bytes_per_launch": nbytes,
+            "us_with_q8": round(whole_us, 3), "achieved_gbs": round(g, 1), "frac": round(g / HBM_PEAK_GBS, 4),
+            "us_gemv_alone": round(alone_us, 3), "achieved_gbs_gemv_alone": round(ga, 1),
+            "frac_gemv_alone": round(ga / HBM_PEAK_GBS, 4)}
 
 
 def bench_prefill(b, model, spec):
@@ -100,53 +124,90 @@ def bench_prefill(b, model, spec):
                           "tok_s": round(sb["prefill_tokens"] / (sb["prefill_ms"] / 1000.0), 1)}}
 
 
-def bench_long_context(b, model, n_fill, steps, wbytes):
-    """Decode after N(0,1) K/V for positions 0..n_fill-1 (seed 4242)."""
-    eng = pih.HipEngine(b, model, n_ctx=n_fill + steps + 16)
+def bench_long_context(b, model, n_fill, n_gen, wbytes):
+    """n_gen greedy tokens after N(0,1) K/V at positions 0..n_fill-1 (seed 4242)."""
+    eng = pih.HipEngine(b, model, n_ctx=n_fill + n_gen + 16)
     eng.kv_fill_normal(n_fill, 4242)
     eng.kv_set_tokens([0] * n_fill)
-    _, st = eng.generate([0] * n_fill + [17], steps + 1)   # reuses n_fill, evaluates token 17, then decodes
+    b.time_kernels(True)
+    _, st = eng.generate([0] * n_fill + [17], n_gen)   # reuses n_fill, evaluates token 17, then decodes
+    kern_us, kern_n = eng.last_kernel_us()
+    b.time_kernels(False)
     tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
-    kv_bytes = 737280 * (n_fill + steps // 2)
+    # forward j (1..n_gen-1) sits at position n_fill + j and reads positions 0..n_fill + j
+    kv_bytes = KV_BYTES_PER_POS * (n_fill + 1 + n_gen / 2)
     per_tok = wbytes + kv_bytes
     return {"context": n_fill, "tok_s": round(tps, 2), "gen_tokens": st["gen_tokens"],
-            "device_us_per_forward": round(eng.last_decode_us(), 1), "reused": st["prefill_cached_tokens"],
-            "bytes_per_token": per_tok, "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
-            "frac": round(tps * per_tok / (HBM_PEAK_GBS * 1e9), 4)}
+            "forwards": kern_n, "kernel_us_per_forward": round(kern_us, 1),
+            "reused": st["prefill_cached_tokens"], "bytes_per_forward": round(per_tok),
+            "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
+            "frac": round(tps * per_tok / (HBM_PEAK_GBS * 1e9), 4),
+            "kernel_gbs": round(per_tok / (kern_us * 1e-6) / 1e9, 1) if kern_us else None}
 
 
 def profile_gemv(b):
     """Q4_K GEMV launches over 70 weight copies and one 256 MiB device copy:
     a short program for rocprofv3 counter runs (FETCH_SIZE / WRITE_SIZE)."""
-    us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 210)
+    us, alone = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 210)
     n = 256 << 20
     src, dst = b.alloc(n), b.alloc(n)
     b.copy_d2d(dst, src, n)
     b.synchronize()
-    print(json.dumps({"profile": "gemv", "q4k_us_per_launch": round(us, 3), "copy_bytes": n}), flush=True)
+    print(json.dumps({"profile": "gemv", "q4k_us_with_q8": round(us, 3), "q4k_us_alone": round(alone, 3),
+                      "copy_bytes": n}), flush=True)
+
+
+def profile_decode(b, model, prompt):
+    """One 32-token decode of the config-3 model and one 256 MiB device copy:
+    a short program for rocprofv3 counter runs on k_mega."""
+    eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + 40)
+    ids, st = eng.generate(prompt, 32)
+    n = 256 << 20
+    src, dst = b.alloc(n), b.alloc(n)
+    b.copy_d2d(dst, src, n)
+    b.synchronize()
+    print(json.dumps({"profile": "decode", "gen_tokens": st["gen_tokens"], "gen_ms": round(st["gen_ms"], 2),
+                      "copy_bytes": n}), flush=True)
 
 
 def cpu_baseline(model, prompt):
+    """The oracle (the reference's CPU path restated) on the host's cores."""
     from oracle import oracle
-    threads = min(os.cpu_count() or 1, 16)
-    eng = oracle.OracleEngine(model, n_ctx=64, threads=threads)
-    ids, st = eng.generate(prompt[:32], 9)
-    eng.close()
-    tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
-    return {"value": round(tps, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle greedy decode of the same model: 32-id prompt, {st['gen_tokens']} tokens "
-                      f"({st['gen_tokens'] - 1} forwards, {st['gen_ms']:.0f} ms); prefill {st['prefill_ms']:.0f} ms"}
+    nproc = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else nproc
+    all_threads = max(1, min(avail, 16))
+
+    def run(threads, n_prompt, n_tok, int8=True):
+        eng = oracle.OracleEngine(model, n_ctx=64, threads=threads)
+        eng.set_int8(int8)
+        _, st = eng.generate(prompt[:n_prompt], n_tok)
+        eng.close()
+        return {"threads": threads, "tok_s": round(st["gen_tokens"] / (st["gen_ms"] / 1000.0), 3),
+                "gen_tokens": st["gen_tokens"], "gen_ms": round(st["gen_ms"], 1),
+                "prefill_tokens": n_prompt, "prefill_ms": round(st["prefill_ms"], 1)}
+
+    t4 = run(4, 32, 12)
+    ta = run(all_threads, 32, 16)
+    f32 = run(all_threads, 8, 4, int8=False)
+    return {"value": ta["tok_s"], "unit": "tok/s", "cores": all_threads, "kind": "port",
+            "nproc": nproc, "available_cores": avail,
+            "sample": f"oracle int8 greedy decode of the same model (the reference's aarch64 CPU path restated): "
+                      f"32-id prompt, {ta['gen_tokens']} tokens ({ta['gen_tokens'] - 1} forwards) at "
+                      f"{all_threads} threads; 12 tokens at 4 threads; f32 path (quant.rs:377-476): 8-id prompt, "
+                      f"4 tokens",
+            "threads_4": t4, "threads_all": ta, "f32_path_threads_all": f32}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=255, help="timed decode forwards (tokens = steps + 1)")
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=3, help="timed full decodes (128-id prompt + 256 tokens each)")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed full decodes first")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graphs", action="store_true", help="launch kernels one by one (for profilers)")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill and long-context sections")
     ap.add_argument("--profile-gemv", action="store_true", help="GEMV launches and a device copy only")
+    ap.add_argument("--profile-decode", action="store_true", help="one 32-token decode and a device copy only")
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV measurements")
     ap.add_argument("--skip", default="", help="comma list of sections to leave out: gemv,decode,prefill,long,cpu")
     args = ap.parse_args()
@@ -157,61 +218,84 @@ def main():
         print("bench.py runs on one MI355X only: multi-GPU runs are not part of this build "
               "(the sharding plan is described in DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
     t_start = time.time()
     b = pih.HipBackend(0)
+    try:
+        run(args, skip, steps, warmup, b, t_start)
+    finally:
+        b.close()
+
+
+def run(args, skip, steps, warmup, b, t_start):
     b.use_graphs(not args.no_graphs)
     log(f"device: {b.name()}")
     if args.profile_gemv:
         profile_gemv(b)
         return
 
-    # -- roofline: dominant kernel, config-1 shape, HBM-cold -----------------
-    q4k_us = q6k_us = float("nan")
+    # -- standalone GEMVs of configs 1 and 2, HBM-cold ----------------------
+    g4 = g6 = None
     if not args.no_gemv:
-        q4k_us = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
-        q6k_us = time_gemv(b, pih.Q6_K, Q6K_ROWS, Q6K_K, pih.synth_q6k_random, 3, 30)
-    q4k_gbs = Q4K_LAUNCH_BYTES / (q4k_us * 1e-6) / 1e9
-    log(f"Q4_K GEMV {Q4K_ROWS}x{Q4K_K}: {q4k_us:.2f} us/launch, {q4k_gbs:.0f} GB/s")
-    q6k_gbs = Q6K_LAUNCH_BYTES / (q6k_us * 1e-6) / 1e9
-    log(f"Q6_K GEMV {Q6K_ROWS}x{Q6K_K}: {q6k_us:.2f} us/launch, {q6k_gbs:.0f} GB/s")
+        w4, a4 = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
+        w6, a6 = time_gemv(b, pih.Q6_K, Q6K_ROWS, Q6K_K, pih.synth_q6k_random, 3, 30)
+        g4 = gemv_entry(w4, a4, Q4K_LAUNCH_BYTES, "Q4_K GEMV 5760x2304: k_q8 + k_gemv<12,1,0>")
+        g4["traffic_gemv_alone"] = Q4K_TRAFFIC_BYTES
+        g6 = gemv_entry(w6, a6, Q6K_LAUNCH_BYTES, "Q6_K head GEMV 122753x2304: k_q8 + k_gemv<14,1,0>")
+        log(f"gemv q4k: {g4}")
+        log(f"gemv q6k: {g6}")
 
-    # -- decode ------------------------------------------------------------
+    # -- decode (config 3) ----------------------------------------------------
     spec = pih.minicpm2b_spec()
     t0 = time.time()
     model = pih.synth_model(spec, MODEL_SEED)
-    log(f"model synthesized in {time.time() - t0:.1f}s; {model.weight_bytes_per_token()} weight bytes/token")
-    prompt = splitmix_ids(PROMPT_SEED, N_PROMPT, spec.n_vocab)
-    n_tokens = args.steps + 1
-    if "decode" in skip:
-        ids, st = [], {"gen_tokens": 1, "gen_ms": float("nan"), "stop": "skipped", "prefill_ms": 0.0,
-                       "prefill_cached_tokens": 0}
-        eng = None
-    else:
-        eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + max(n_tokens, args.warmup + 1) + 8)
-        eng.generate(prompt, args.warmup + 1)
-        b.synchronize()
-        ids, st = eng.generate(prompt, n_tokens)
-        b.synchronize()
-    fwd = max(st["gen_tokens"] - 1, 1)
-    tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
-    dev_us = eng.last_decode_us() if eng else float("nan")
     wbytes = model.weight_bytes_per_token()
-    log(f"decode: {st['gen_tokens']} tokens in {st['gen_ms']:.1f} ms ({tps:.1f} tok/s), "
-        f"device {dev_us:.1f} us/forward, stop={st['stop']}, prefill {st['prefill_ms']:.1f} ms "
-        f"({st['prefill_cached_tokens']} reused)")
-    golden = REPO / "tests" / "golden" / "minicpm2b_greedy.json"
-    match = None
-    if golden.exists():
-        g = json.loads(golden.read_text())
-        if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED and len(ids) >= g["n_gen"]:
-            match = ids[: g["n_gen"]] == g["gen_ids"]
+    log(f"model synthesized in {time.time() - t0:.1f}s; {wbytes} weight bytes/token")
+    prompt = splitmix_ids(PROMPT_SEED, N_PROMPT, spec.n_vocab)
+    if args.profile_decode:
+        profile_decode(b, model, prompt)
+        return
+    runs, match, kern = [], None, []
+    eng = None
+    if "decode" not in skip:
+        eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + N_GEN + 8)
+        for _ in range(warmup):
+            eng.generate(prompt, N_GEN)
+        b.synchronize()
+        b.time_kernels(True)
+        for i in range(steps):
+            ids, st = eng.generate(prompt, N_GEN)
+            runs.append(st)
+            kern.append(eng.last_kernel_us())
+            log(f"decode {i}: {st['gen_tokens']} tokens in {st['gen_ms']:.1f} ms "
+                f"({st['gen_tokens'] / st['gen_ms'] * 1000:.1f} tok/s), k_mega {kern[-1][0]:.1f} us/launch, "
+                f"stop={st['stop']}, prefill {st['prefill_ms']:.1f} ms ({st['prefill_cached_tokens']} reused)")
+            if i == 0:
+                golden = REPO / "tests" / "golden" / "minicpm2b_greedy.json"
+                if golden.exists():
+                    g = json.loads(golden.read_text())
+                    if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED and len(ids) >= g["n_gen"]:
+                        match = ids[: g["n_gen"]] == g["gen_ids"]
+        b.time_kernels(False)
+    gen_tokens = sum(st["gen_tokens"] for st in runs)
+    gen_ms = sum(st["gen_ms"] for st in runs)
+    fwd = sum(max(st["gen_tokens"] - 1, 0) for st in runs)
+    tps = gen_tokens / (gen_ms / 1000.0) if runs else float("nan")
+    kern_n = sum(n for _, n in kern)
+    kern_us = sum(u * n for u, n in kern) / kern_n if kern_n else float("nan")
+    # forward j (1..255) evaluates position 127 + j and reads the KV of
+    # positions 0..127 + j: 128 + j rows, mean 256
+    n_fwd = N_GEN - 1
+    kv_mean = KV_BYTES_PER_POS * sum(N_PROMPT + j for j in range(1, n_fwd + 1)) / n_fwd
+    launch_bytes = wbytes + kv_mean + EMBD_ROW_BYTES
+    mega_gbs = launch_bytes / (kern_us * 1e-6) / 1e9
 
     prefill = long_ctx = None
     if not args.no_extra and "prefill" not in skip:
         prefill = bench_prefill(b, model, spec)
         log(f"prefill: {prefill}")
     if not args.no_extra and "long" not in skip:
-        long_ctx = [bench_long_context(b, model, n, 16, wbytes) for n in (4096, 16384)]
+        long_ctx = [bench_long_context(b, model, n, 64, wbytes) for n in (4096, 16384)]
         log(f"long context: {long_ctx}")
 
     cpu = None
@@ -220,31 +304,33 @@ def main():
         log(f"cpu baseline: {cpu}")
 
     out = {
-        "metric": "decode tok/s, 2B Q4_K_M synthetic",
+        "metric": METRIC,
         "value": round(tps, 2),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": fwd,
-        "warmup": args.warmup,
-        "ms_per_step": round(st["gen_ms"] / fwd, 4),
+        "steps": len(runs),
+        "warmup": warmup,
+        "ms_per_step": round(gen_ms / max(len(runs), 1), 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 dot / f32",
         "data": "synthetic (seeded random weights N(0,0.02) quantized Q4_K_M-style, random prompt ids)",
         "config": {"workload": "greedy decode, MiniCPM-2B-shaped Q4_K_M synthetic model: 40 layers, "
-                               "hidden 2304, 36x64 MHA, FFN 5760, vocab 122753, f32 KV",
-                   "prompt_tokens": N_PROMPT, "gen_tokens": st["gen_tokens"], "batch": 1},
-        "roofline": {"bound": "hbm", "achieved": round(q4k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(q4k_gbs / HBM_PEAK_GBS, 4), "traffic": Q4K_TRAFFIC_BYTES,
-                     "kernel": "Q4_K GEMV 5760x2304 (k_gemv<12,1,0>)", "us_per_launch": round(q4k_us, 3),
-                     "bytes_per_launch": Q4K_LAUNCH_BYTES},
-        "q6k_head_gemv": {"achieved": round(q6k_gbs, 1), "unit": "GB/s", "frac": round(q6k_gbs / HBM_PEAK_GBS, 4),
-                          "us_per_launch": round(q6k_us, 3), "bytes_per_launch": Q6K_LAUNCH_BYTES},
+                               "hidden 2304, 36x64 MHA, FFN 5760, vocab 122753, f32 KV; one step = 128-id "
+                               "prompt then 256 greedy tokens (255 forwards) at batch 1",
+                   "prompt_tokens": N_PROMPT, "gen_tokens": runs[0]["gen_tokens"] if runs else 0, "batch": 1,
+                   "forwards_timed": fwd, "ms_per_forward": round(gen_ms / fwd, 4) if fwd else None},
+        "roofline": {"bound": "hbm", "achieved": round(mega_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(mega_gbs / HBM_PEAK_GBS, 4), "traffic": K_MEGA_TRAFFIC_BYTES,
+                     "kernel": "k_mega (persistent decode kernel, one launch per decode forward)",
+                     "us_per_launch": round(kern_us, 2), "launches_timed": kern_n,
+                     "bytes_per_launch": round(launch_bytes), "weight_bytes": wbytes,
+                     "kv_bytes_mean": round(kv_mean),
+                     "gemv_q4k": g4, "gemv_q6k": g6},
         "decode_weight_roofline": {"weight_bytes_per_token": wbytes,
                                    "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
-                                   "frac": round(tps * wbytes / (HBM_PEAK_GBS * 1e9), 4),
-                                   "device_us_per_forward": round(dev_us, 2)},
+                                   "frac": round(tps * wbytes / (HBM_PEAK_GBS * 1e9), 4)},
         "greedy_first_64_match_oracle": match,
         "prefill": prefill,
         "long_context": long_ctx,

@@ -90,8 +90,10 @@ void pi_hip_tensor_free(pi_ctx *ctx, pi_tensor *t);
 /* Bytes the tensor occupies in HBM (the algorithmic weight bytes). */
 size_t pi_hip_tensor_bytes(const pi_tensor *t);
 /* y[rows] = W x with x and y device pointers, on the context stream.
- * Quantizes x (k floats) to Q8 blocks on the device first (quant_int.rs:17-56),
- * then runs the fused dequant + int8-dot GEMV (quant_int.rs:330-419). */
+ * One launch: every workgroup quantizes x (k floats) to Q8 blocks in its LDS
+ * (quant_int.rs:17-56), then runs the fused dequant + int8-dot GEMV
+ * (quant_int.rs:330-419).  (Rows too long for LDS take a Q8 pre-pass into
+ * context staging memory instead; same results.) */
 int  pi_hip_gemv_dev(pi_ctx *ctx, const pi_tensor *w, const float *x_dev, float *y_dev);
 /* Same GEMV on already-quantized activations (device pointers, lane 0). */
 int  pi_hip_gemv_q8_dev(pi_ctx *ctx, const pi_tensor *w, const int8_t *q_dev, const float *d_dev,
@@ -103,6 +105,13 @@ int  pi_hip_gemv_q8_dev(pi_ctx *ctx, const pi_tensor *w, const int8_t *q_dev, co
 int  pi_hip_time_gemv(pi_ctx *ctx, const pi_tensor *const *weights, int n_copies, const int8_t *q_dev,
                       const float *d_dev, const int32_t *sum_dev, float *y_dev, int iters,
                       double *avg_us);
+
+/* Times `iters` runs of the whole pi_hip_gemv_dev job (Q8 of the f32 x in
+ * HBM, then the GEMV) with HIP events on the context stream; writes the mean
+ * time per run in microseconds.  Weight copies rotate as in pi_hip_time_gemv.
+ * No counterpart in the reference (its matvec times nothing, opencl.rs:436-500). */
+int  pi_hip_time_gemv_x(pi_ctx *ctx, const pi_tensor *const *weights, int n_copies, const float *x_dev,
+                        float *y_dev, int iters, double *avg_us);
 
 /* Q8Act::prepare on device buffers (x feature-major [k][b]), context stream. */
 int  pi_hip_q8_quantize_dev(pi_ctx *ctx, const float *x_dev, size_t k, int b, int8_t *q_dev, float *d_dev,
@@ -234,8 +243,15 @@ int  pi_hip_persistent_active(const pi_ctx *ctx);
  * reports blocks and slots. */
 int  pi_hip_stage_trace(pi_ctx *ctx, int enable);
 int  pi_hip_stage_trace_read(pi_ctx *ctx, uint64_t *out, size_t n, uint32_t *blocks, uint32_t *slots);
-/* Per-forward timing of the last generate call, microseconds (device events). */
+/* Per-forward timing of the last generate call, microseconds (device events
+ * around the whole decode loop, host waits included). */
 int  pi_hip_last_decode_us(pi_ctx *ctx, double *per_token_us);
+/* Kernel timing of generate (the reference's GenStats timing, model.rs:666-676,
+ * at kernel granularity): when enabled, every decode forward is bracketed by
+ * an event pair, and pi_hip_last_kernel_us reports the mean device time of
+ * one forward's kernels over the n forwards of the last generate call. */
+int  pi_hip_time_kernels(pi_ctx *ctx, int enable);
+int  pi_hip_last_kernel_us(pi_ctx *ctx, double *per_forward_us, uint32_t *n);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic data (host-side, deterministic across machines: integer

@@ -69,6 +69,8 @@ struct Engine {
     std::vector<uint32_t> kv_tokens;
     size_t cached_prefill_len = 0;
     double last_decode_us = 0.0;
+    double last_kernel_us = 0.0;    // mean device time of one decode forward's kernels (kernel timing on)
+    uint32_t last_kernel_n = 0;
     // persistent decode kernel (pi_mega.hip)
     bool mega_ok = false;           // the model fits the kernel
     pi_mega_args mega{};            // host copy of the device-resident arguments
@@ -100,6 +102,7 @@ struct pi_ctx {
     bool use_graphs = true;   // replay captured graphs (else launch each kernel)
     bool use_persistent = true;  // one persistent kernel per token when the model fits
     bool use_batch_prefill = true;  // chunks of 2..32 tokens on the MFMA prefill kernels
+    bool time_kernels = false;      // event pair around every decode forward of generate
     std::atomic<int> stop{0};
     std::map<std::pair<uintptr_t, size_t>, pi_tensor *> wcache;
     // grow-only IO buffers of matvec / test hooks (opencl.rs:461-482)
@@ -108,6 +111,7 @@ struct pi_ctx {
     float *io_d = nullptr;
     int32_t *io_s = nullptr;
     size_t cap_x = 0, cap_y = 0;
+    int max_lds = 65536;      // LDS bytes a workgroup may use on this device
     Engine *eng = nullptr;
 };
 
@@ -725,6 +729,9 @@ int pi_hip_create(pi_ctx **out, int device) {
         return PI_E_HIP;
     }
     c->stream = c->own;
+    int lds = 0;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeSharedMemPerBlockOptin, device) == hipSuccess && lds > 0)
+        c->max_lds = lds;
     char buf[300];
     snprintf(buf, sizeof buf, "HIP %s (%s)", p.name, p.gcnArchName);
     c->name = buf;
@@ -842,14 +849,26 @@ int pi_hip_gemv_q8_dev(pi_ctx *c, const pi_tensor *w, const int8_t *q, const flo
     return PI_OK;
 }
 
-int pi_hip_gemv_dev(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
-    if (!c || !w || !x || !y) return PI_E_INVALID;
-    if (take_injected(c)) return PI_E_INJECTED;
+// y = W x for an f32 x in HBM (the whole job of pi_hip_gemv_dev): one
+// launch whose workgroups each quantize x into LDS; for rows too long for
+// that LDS, Q8 of x into the context's staging buffers, then the GEMV.
+static int enqueue_gemv_x(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
+    if (pi_gemv_x_lds_bytes(w->L.type, w->L.g, w->L.k) <= (size_t)c->max_lds) {
+        const pi_matset M = make_set({{w, y}});
+        HIPC(c, pi_launch_gemv_x(M, x, gemv_blocks(w->L.ntiles), c->stream));
+        return PI_OK;
+    }
     int r = grow_io(c, w->L.k, 1);
     if (r) return r;
     HIPC(c, pi_launch_q8(x, w->L.k, 1, c->io_q, c->io_d, c->io_s, c->stream));
     HIPC(c, launch_single_gemv(w, c->io_q, c->io_d, c->io_s, y, nullptr, PI_GEMV_OUT, c->stream));
     return PI_OK;
+}
+
+int pi_hip_gemv_dev(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
+    if (!c || !w || !x || !y) return PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    return enqueue_gemv_x(c, w, x, y);
 }
 
 int pi_hip_q8_quantize_dev(pi_ctx *c, const float *x, size_t k, int b, int8_t *q, float *d, int32_t *s) {
@@ -920,6 +939,29 @@ int pi_hip_time_gemv(pi_ctx *c, const pi_tensor *const *ws, int n_copies, const 
     return PI_OK;
 }
 
+int pi_hip_time_gemv_x(pi_ctx *c, const pi_tensor *const *ws, int n_copies, const float *x, float *y, int iters,
+                       double *avg_us) {
+    if (!c || !ws || n_copies < 1 || iters < 1 || !x || !y || !avg_us) return PI_E_INVALID;
+    for (int i = 0; i < n_copies; i++)
+        if (!ws[i] || ws[i]->L.k != ws[0]->L.k) return fail(c, PI_E_INVALID, "weight copies differ in row length");
+    int r = grow_io(c, ws[0]->L.k, 1);
+    if (r) return r;
+    hipEvent_t a, b;
+    HIPC(c, hipEventCreate(&a));
+    HIPC(c, hipEventCreate(&b));
+    HIPC(c, hipEventRecord(a, c->stream));
+    for (int i = 0; i < iters; i++)
+        if ((r = enqueue_gemv_x(c, ws[i % n_copies], x, y))) return r;
+    HIPC(c, hipEventRecord(b, c->stream));
+    HIPC(c, hipEventSynchronize(b));
+    float ms = 0.f;
+    HIPC(c, hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    *avg_us = (double)ms * 1000.0 / iters;
+    return PI_OK;
+}
+
 int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, size_t k, const float *x, float *out,
                   size_t rows) {
     if (!c || !w || !x || !out || rows == 0 || k == 0) return c ? fail(c, PI_E_INVALID, "invalid matvec arguments") : PI_E_INVALID;
@@ -941,8 +983,7 @@ int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, si
     int r = grow_io(c, k, rows);
     if (r) return r;
     HIPC(c, hipMemcpyAsync(c->io_x, x, k * 4, hipMemcpyHostToDevice, c->stream));
-    HIPC(c, pi_launch_q8(c->io_x, (uint32_t)k, 1, c->io_q, c->io_d, c->io_s, c->stream));
-    HIPC(c, launch_single_gemv(t, c->io_q, c->io_d, c->io_s, c->io_y, nullptr, PI_GEMV_OUT, c->stream));
+    if ((r = enqueue_gemv_x(c, t, c->io_x, c->io_y))) return r;
     HIPC(c, hipMemcpyAsync(out, c->io_y, rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
     return PI_OK;
@@ -1259,6 +1300,19 @@ int pi_hip_last_decode_us(pi_ctx *c, double *us) {
     return PI_OK;
 }
 
+int pi_hip_time_kernels(pi_ctx *c, int enable) {
+    if (!c) return PI_E_INVALID;
+    c->time_kernels = enable != 0;
+    return PI_OK;
+}
+
+int pi_hip_last_kernel_us(pi_ctx *c, double *us, uint32_t *n) {
+    if (!c || !us || !n || !c->eng) return PI_E_INVALID;
+    *us = c->eng->last_kernel_us;
+    *n = c->eng->last_kernel_n;
+    return PI_OK;
+}
+
 int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopts *o, pi_genstats *st,
                     uint32_t *gen_ids) {
     if (!c || !o || !st) return PI_E_INVALID;
@@ -1381,19 +1435,50 @@ prefill_done:
     const size_t want_fwd = std::min(fwd_cap, ctx_cap);
     size_t i = 0;
     bool done = (max_gen == 0);
+    // Kernel timing: an event pair around every decode forward; the mean of
+    // their elapsed times is the device time of one forward's kernels.
+    std::vector<hipEvent_t> kev;
+    if (c->time_kernels) {
+        kev.resize(2 * kDecodeChunk, nullptr);
+        for (hipEvent_t &x : kev) HIPC(c, hipEventCreate(&x));
+    }
+    double kern_ms = 0.0;
+    auto free_kev = [&] {
+        for (hipEvent_t x : kev)
+            if (x) (void)hipEventDestroy(x);
+        kev.clear();
+    };
+    // The first id comes from the prompt's last forward: it is checked before
+    // any decode forward is launched, so an immediate EOG leaves that
+    // forward's logits in place (as Engine::generate does, model.rs:1305-1306).
+    if (!done) {
+        uint32_t first = 0;
+        HIPC(c, hipMemcpyAsync(&first, e->ids, 4, hipMemcpyDeviceToHost, c->stream));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        for (uint32_t x : e->eos) done |= (x == first);
+        if (done) snprintf(st->stop, sizeof st->stop, "eog");
+    }
     while (!done) {
         // launch up to kDecodeChunk forwards ahead, then read the ids back
         size_t target = std::min(want_fwd, launched + kDecodeChunk);
+        const size_t base = launched;
         while (launched < target) {
+            if (!kev.empty()) HIPC(c, hipEventRecord(kev[2 * (launched - base)], c->stream));
             if (mega)
                 HIPC(c, mega_token(c, *e, (int32_t)(n + launched), 0, &e->st->tok, e->ids + launched + 1, true, true));
             else HIPC(c, run_step(c, *e, STEP_DECODE));
+            if (!kev.empty()) HIPC(c, hipEventRecord(kev[2 * (launched - base) + 1], c->stream));
             launched++;
         }
         host_ids.resize(launched + 1);
         HIPC(c, hipMemcpyAsync(host_ids.data(), e->ids, (launched + 1) * 4, hipMemcpyDeviceToHost, c->stream));
         HIPC(c, hipStreamSynchronize(c->stream));
-        if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); e->cached_prefill_len = 0; return r; }
+        if ((r = mega_check(c, *e))) { free_kev(); e->kv_tokens.clear(); e->cached_prefill_len = 0; return r; }
+        for (size_t j = 0; j < launched - base && !kev.empty(); j++) {
+            float ms = 0.f;
+            HIPC(c, hipEventElapsedTime(&ms, kev[2 * j], kev[2 * j + 1]));
+            kern_ms += ms;
+        }
         while (!done && i <= launched) {
             if (c->stop.load()) { snprintf(st->stop, sizeof st->stop, "user_stop"); done = true; break; }
             const uint32_t tok = host_ids[i];
@@ -1413,7 +1498,28 @@ prefill_done:
     HIPC(c, hipEventElapsedTime(&ms, ea, eb));
     (void)hipEventDestroy(ea);
     (void)hipEventDestroy(eb);
+    free_kev();
     e->last_decode_us = launched ? (double)ms * 1000.0 / (double)launched : 0.0;
+    e->last_kernel_us = (c->time_kernels && launched) ? kern_ms * 1000.0 / (double)launched : 0.0;
+    e->last_kernel_n = c->time_kernels ? (uint32_t)launched : 0u;
+    // An EOG sampled after i >= 1 forwards may have been read after later
+    // forwards were already launched.  Forward i (token i-1 at position
+    // n+i-1) is evaluated again: it writes the same KV row bit for bit and
+    // leaves the logits and greedy id that produced the EOG, which is what
+    // Engine::generate leaves behind (model.rs:1299-1337).
+    if (strcmp(st->stop, "eog") == 0 && i >= 1 && launched > i) {
+        const int32_t p = (int32_t)(n + i - 1);
+        const uint32_t tk = host_ids[i - 1];
+        if (mega) {
+            HIPC(c, mega_token(c, *e, p, tk, nullptr, nullptr, true, true));
+        } else {
+            if ((r = set_state(c, *e, p, tk, 0, 0))) return r;
+            HIPC(c, enqueue_step(*e, PI_STEP_EMBED, nullptr, c->stream));
+            HIPC(c, run_step(c, *e, STEP_DECODE));
+        }
+        HIPC(c, hipStreamSynchronize(c->stream));
+        if ((r = mega_check(c, *e))) { e->kv_tokens.clear(); e->cached_prefill_len = 0; return r; }
+    }
     // Forwards launched past an EOS or stop only wrote KV rows beyond the
     // recorded tokens; they are never read before being overwritten.
     e->kv_tokens.resize(std::min(e->kv_tokens.size(), n + (size_t)st->gen_tokens));

@@ -70,6 +70,11 @@ struct pi_attn_args {
 // n == 1): `blocks` persistent wavefronts, four per workgroup.
 hipError_t pi_launch_gemv_set(const pi_matset &M, const int8_t *aq, const float *ad, const int32_t *as,
                               int32_t *sums, int mode, uint32_t blocks, hipStream_t s);
+// Standalone GEMV on an f32 x (k floats in HBM): each workgroup quantizes x
+// to Q8 blocks in its LDS, then runs the tiles (mode OUT).
+hipError_t pi_launch_gemv_x(const pi_matset &M, const float *x, uint32_t blocks, hipStream_t s);
+// LDS bytes of that kernel for a layout (type, units of g blocks, row length k).
+size_t pi_gemv_x_lds_bytes(uint32_t type, uint32_t g, uint32_t k);
 hipError_t pi_launch_norm_gemv(const pi_norm_gemv_args &a, bool neon, hipStream_t s);
 hipError_t pi_launch_gemv_res(const pi_gemv_res_args &a, hipStream_t s);
 hipError_t pi_launch_attn(const pi_attn_args &a, bool neon, hipStream_t s);

@@ -316,6 +316,59 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(MatSet S, const int8_t *_
     }
 }
 
+// Row bytes of the LDS copy of a Q8 activation of k elements: quant chunks
+// in act_chunk order need whole 256-byte rows.
+__host__ __device__ constexpr uint32_t act_q_bytes(uint32_t k) { return (k + 255u) & ~255u; }
+
+// Standalone GEMV on an f32 x in HBM: every workgroup forms the Q8
+// activation of x itself (Q8Act::prepare, quant_int.rs:17-56: the pair rule
+// of q8_pair_core, bit-identical to the oracle) into LDS, so one launch does
+// the whole job of quantize-then-multiply.  Each wavefront requests the
+// weights of its first tile before it reads x, so that latency overlaps the
+// quantization.  y[m][row] = sum of terms in the reference's order.
+template <uint32_t T, int G>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_x(MatSet S, const float *__restrict__ x, uint32_t k) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    constexpr int TPU = QT<T>::TPB * G;
+    constexpr uint32_t W = kGemvThreads / 64;
+    float *strips = reinterpret_cast<float *>(smem);
+    unsigned char *act = smem + ((W * 64 * TPU + kChainPad) * 4 + 15) / 16 * 16;
+    uint32_t *qw = reinterpret_cast<uint32_t *>(act);
+    float *ad = reinterpret_cast<float *>(act + act_q_bytes(k));
+    int32_t *as = reinterpret_cast<int32_t *>(ad + k / 32);
+    const uint32_t lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t gw = blockIdx.x * W + wave, nw = gridDim.x * W;
+    const bool has = gw < S.tile0[3];
+    Unit<T, G> UA;
+    TileRef RA{};
+    if (has) {
+        RA = tile_ref(S, gw);
+        UA.load(RA.base, RA.lanes, min(lane, RA.lanes - 1));
+    }
+    // 16 elements per lane, the two halves of a block in adjacent lanes
+    for (uint32_t t = threadIdx.x; t < k / 16; t += kGemvThreads) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + 16 * (uint64_t)t);
+        float v[16];
+#pragma unroll
+        for (int j4 = 0; j4 < 4; j4++) {
+            const float4 q = x4[j4];
+            v[4 * j4 + 0] = q.x;
+            v[4 * j4 + 1] = q.y;
+            v[4 * j4 + 2] = q.z;
+            v[4 * j4 + 3] = q.w;
+        }
+        const uint32_t b = t >> 1, h = t & 1u;
+        q8_pair(v, h, qw + 4 * act_chunk(2 * b + h), ad + b, as + b);
+    }
+    __syncthreads();
+    if (!has) return;
+    Slice<T, G> SL;
+    SL.load_swz(reinterpret_cast<const int8_t *>(qw), ad, as, lane % S.upr);
+    float *strip = strips + wave * 64 * TPU;
+    auto out = [&](uint32_t m, uint32_t row, float v) { S.y[m][row] = v; };
+    run_tiles_pre<T, G>(S, SL, UA, RA, gw, nw, strip, out);
+}
+
 // ---------------------------------------------------------------------------
 // Attention of one head (model.rs:953-1087) for the token at st->pos.
 // RoPE over adjacent pairs with the cached cos/sin, the K/V row write
@@ -596,6 +649,36 @@ hipError_t launch_gemv_g(const pi_matset &M, const int8_t *aq, const float *ad, 
     return hipGetLastError();
 }
 
+template <uint32_t T, int G>
+hipError_t launch_gemv_x_g(const pi_matset &M, const float *x, uint32_t blocks, hipStream_t s) {
+    const MatSet S = to_set(M);
+    constexpr uint32_t TPU = QT<T>::TPB * G;
+    const size_t shm = (((kGemvThreads / 64) * 64 * TPU + kChainPad) * 4 + 15) / 16 * 16 + act_q_bytes(M.L.k) +
+                       (size_t)(M.L.k / 32) * 8;
+    const dim3 grid((blocks + kGemvThreads / 64 - 1) / (kGemvThreads / 64)), blk(kGemvThreads);
+    hipError_t e = hipFuncSetAttribute((const void *)k_gemv_x<T, G>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((k_gemv_x<T, G>), grid, blk, shm, s, S, x, M.L.k);
+    return hipGetLastError();
+}
+
+template <uint32_t T>
+hipError_t launch_gemv_x_t(const pi_matset &M, const float *x, uint32_t blocks, hipStream_t s) {
+    if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) {
+        return M.L.g == 1 ? launch_gemv_x_g<T, 1>(M, x, blocks, s) : hipErrorInvalidValue;
+    } else {
+        switch (M.L.g) {
+        case 1: return launch_gemv_x_g<T, 1>(M, x, blocks, s);
+        case 2: return launch_gemv_x_g<T, 2>(M, x, blocks, s);
+        case 3: return launch_gemv_x_g<T, 3>(M, x, blocks, s);
+        case 4: return launch_gemv_x_g<T, 4>(M, x, blocks, s);
+        case 6: return launch_gemv_x_g<T, 6>(M, x, blocks, s);
+        case 8: return launch_gemv_x_g<T, 8>(M, x, blocks, s);
+        default: return hipErrorInvalidValue;
+        }
+    }
+}
+
 template <uint32_t T>
 hipError_t launch_gemv_t(const pi_matset &M, const int8_t *aq, const float *ad, const int32_t *as, int32_t *sums,
                          int mode, uint32_t blocks, hipStream_t s) {
@@ -625,6 +708,22 @@ hipError_t pi_launch_gemv_set(const pi_matset &M, const int8_t *aq, const float 
     case PI_TYPE_Q6_K: return launch_gemv_t<PI_TYPE_Q6_K>(M, aq, ad, as, sums, mode, blocks, s);
     case PI_TYPE_Q4_0: return launch_gemv_t<PI_TYPE_Q4_0>(M, aq, ad, as, sums, mode, blocks, s);
     case PI_TYPE_Q8_0: return launch_gemv_t<PI_TYPE_Q8_0>(M, aq, ad, as, sums, mode, blocks, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+size_t pi_gemv_x_lds_bytes(uint32_t type, uint32_t g, uint32_t k) {
+    const uint32_t tpu = (type == PI_TYPE_Q4_K ? 8u : type == PI_TYPE_Q6_K ? 16u : 1u) * g;
+    return (((kGemvThreads / 64) * 64 * tpu + kChainPad) * 4 + 15) / 16 * 16 + act_q_bytes(k) + (size_t)(k / 32) * 8;
+}
+
+hipError_t pi_launch_gemv_x(const pi_matset &M, const float *x, uint32_t blocks, hipStream_t s) {
+    if (M.n < 1 || M.n > 3 || blocks == 0 || !x || M.L.k % 32) return hipErrorInvalidValue;
+    switch (M.L.type) {
+    case PI_TYPE_Q4_K: return launch_gemv_x_t<PI_TYPE_Q4_K>(M, x, blocks, s);
+    case PI_TYPE_Q6_K: return launch_gemv_x_t<PI_TYPE_Q6_K>(M, x, blocks, s);
+    case PI_TYPE_Q4_0: return launch_gemv_x_t<PI_TYPE_Q4_0>(M, x, blocks, s);
+    case PI_TYPE_Q8_0: return launch_gemv_x_t<PI_TYPE_Q8_0>(M, x, blocks, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes as C
 import os
+import sys
 from dataclasses import dataclass, field
 from pathlib import Path
 
@@ -45,6 +46,7 @@ EXPORTS = [
     "pi_hip_model_bind", "pi_hip_forward", "pi_hip_logits", "pi_hip_argmax", "pi_hip_generate",
     "pi_hip_kv_write", "pi_hip_kv_read", "pi_hip_kv_fill_normal", "pi_hip_kv_set_tokens",
     "pi_hip_request_stop", "pi_hip_clear_stop", "pi_hip_use_graphs", "pi_hip_last_decode_us",
+    "pi_hip_time_kernels", "pi_hip_last_kernel_us", "pi_hip_time_gemv_x",
     "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
     "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor", "pi_synth_kv_normal",
     "pi_quantize_row",
@@ -143,6 +145,9 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_hip_stage_trace": (i32, [vp, i32]),
         "pi_hip_stage_trace_read": (i32, [vp, vp, C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
         "pi_hip_last_decode_us": (i32, [vp, C.POINTER(C.c_double)]),
+        "pi_hip_time_kernels": (i32, [vp, i32]),
+        "pi_hip_last_kernel_us": (i32, [vp, C.POINTER(C.c_double), C.POINTER(u32)]),
+        "pi_hip_time_gemv_x": (i32, [vp, C.POINTER(vp), i32, vp, vp, i32, C.POINTER(C.c_double)]),
         "pi_synth_q4k_random": (i32, [u64, sz, sz, f32, f32, vp]),
         "pi_synth_q6k_random": (i32, [u64, sz, sz, f32, f32, vp]),
         "pi_synth_normal": (i32, [u64, sz, f32, f32, vp]),
@@ -247,6 +252,10 @@ class Tensor:
             self.handle = 0
 
     def __del__(self):
+        # At interpreter shutdown the HIP runtime (and any profiler attached to
+        # it) may already be finalized: leave the memory to process exit.
+        if sys.is_finalizing():
+            return
         try:
             if self._b.ctx:
                 self.free()
@@ -272,6 +281,10 @@ class DevBuf:
             self.ptr = 0
 
     def __del__(self):
+        # At interpreter shutdown the HIP runtime (and any profiler attached to
+        # it) may already be finalized: leave the memory to process exit.
+        if sys.is_finalizing():
+            return
         try:
             if self._b.ctx:
                 self.free()
@@ -290,6 +303,7 @@ class HipBackend:
             raise PiError(rc, f"no gfx950 device {device}")
         self.ctx = h.value
         self._keep: list = []
+        self.bind_gen = 0   # bumped by every model bind: a context holds one engine
 
     # -- OpenClBackend surface --------------------------------------------
     def name(self) -> str:
@@ -329,6 +343,17 @@ class HipBackend:
         us = C.c_double()
         self.check(self.lib.pi_hip_time_gemv(self.ctx, arr, len(ws), q_ptr, d_ptr, s_ptr, y_ptr, iters, C.byref(us)))
         return us.value
+
+    def time_gemv_x(self, ws: list[Tensor], x_ptr: int, y_ptr: int, iters: int) -> float:
+        """Mean microseconds of the whole gemv_dev job (Q8 of x, then the GEMV)."""
+        arr = (C.c_void_p * len(ws))(*[w.handle for w in ws])
+        us = C.c_double()
+        self.check(self.lib.pi_hip_time_gemv_x(self.ctx, arr, len(ws), x_ptr, y_ptr, iters, C.byref(us)))
+        return us.value
+
+    def time_kernels(self, enable: bool) -> None:
+        """Event pair around every decode forward of generate (see last_kernel_us)."""
+        self.check(self.lib.pi_hip_time_kernels(self.ctx, int(enable)))
 
     def q8_quantize_dev(self, x_ptr: int, k: int, b: int, q_ptr: int, d_ptr: int, s_ptr: int) -> None:
         self.check(self.lib.pi_hip_q8_quantize_dev(self.ctx, x_ptr, k, b, q_ptr, d_ptr, s_ptr))
@@ -409,6 +434,10 @@ class HipBackend:
             self.ctx = None
 
     def __del__(self):
+        # At interpreter shutdown the HIP runtime (and any profiler attached to
+        # it) may already be finalized: leave the memory to process exit.
+        if sys.is_finalizing():
+            return
         try:
             self.close()
         except Exception:
@@ -454,9 +483,12 @@ def minicpm2b_spec() -> ModelSpec:
                      ffn_down_types=tuple(Q8_0 if l % 2 == 0 else Q4_0 for l in range(n)))
 
 
-def tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000) -> ModelSpec:
-    """Small model of the same families (k multiple of 256 for K-quants)."""
-    return ModelSpec(n_layer=n_layer, n_embd=n_embd, n_ff=n_ff, n_head=n_head, n_head_kv=n_head, head_dim=64,
+def tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000, n_head_kv=None, n_rot=0) -> ModelSpec:
+    """Small model of the same families (k multiple of 256 for K-quants).
+    n_head_kv < n_head gives grouped-query attention and n_rot < 64 partial
+    RoPE (Config::from_gguf, model.rs:46-64)."""
+    return ModelSpec(n_layer=n_layer, n_embd=n_embd, n_ff=n_ff, n_head=n_head,
+                     n_head_kv=n_head_kv or n_head, head_dim=64, n_rot=n_rot,
                      n_vocab=n_vocab, eos_ids=(n_vocab - 1,),
                      attn_v_types=tuple(Q6_K if l % 2 == 0 else Q4_K for l in range(n_layer)),
                      ffn_down_types=tuple(Q8_0 if l % 2 == 0 else Q4_0 for l in range(n_layer)),
@@ -531,25 +563,36 @@ class HipEngine:
         desc = ModelDesc(s.n_layer, s.n_embd, s.n_ff, s.n_head, s.n_head_kv, s.head_dim, s.n_rot, s.n_vocab,
                          s.rope_theta, s.rms_eps, self._eos, len(s.eos_ids), _tdesc(T["token_embd.weight"]),
                          _tdesc(T["output.weight"]), _tdesc(T["output_norm.weight"]), self._layers)
+        backend.bind_gen += 1
+        self._gen = backend.bind_gen
         backend.check(backend.lib.pi_hip_model_bind(backend.ctx, C.byref(desc), n_ctx))
 
+    def _live(self) -> None:
+        """A context holds one engine: binding another model frees this one."""
+        if self._gen != self.b.bind_gen:
+            raise RuntimeError("this HipEngine was replaced by a later model bind on the same HipBackend")
+
     def forward(self, ids, positions, want_logits=True) -> None:
+        self._live()
         ids = np.ascontiguousarray(ids, np.uint32)
         pos = np.ascontiguousarray(positions, np.int32)
         self.b.check(self.b.lib.pi_hip_forward(self.b.ctx, _ptr(ids), _ptr(pos), len(ids), int(want_logits)))
 
     def logits(self, n: int | None = None) -> np.ndarray:
+        self._live()
         n = n or self.model.spec.n_vocab
         out = np.empty(n, np.float32)
         self.b.check(self.b.lib.pi_hip_logits(self.b.ctx, _ptr(out), n))
         return out
 
     def argmax(self) -> int:
+        self._live()
         v = C.c_uint32()
         self.b.check(self.b.lib.pi_hip_argmax(self.b.ctx, C.byref(v)))
         return v.value
 
     def generate(self, prompt, max_tokens: int, temp: float = 0.0, top_p: float = 1.0, seed: int = 1):
+        self._live()
         prompt = np.ascontiguousarray(prompt, np.uint32)
         ids = np.zeros(max(1, max_tokens), np.uint32)
         opts = GenOpts(max_tokens, temp, top_p, seed)
@@ -562,17 +605,28 @@ class HipEngine:
         return ids[: st.gen_tokens].tolist(), stats
 
     def last_decode_us(self) -> float:
+        self._live()
         v = C.c_double()
         self.b.check(self.b.lib.pi_hip_last_decode_us(self.b.ctx, C.byref(v)))
         return v.value
 
+    def last_kernel_us(self) -> tuple[float, int]:
+        """(mean device microseconds of one decode forward's kernels, forwards
+        timed) of the last generate call; (0, 0) unless kernel timing is on."""
+        self._live()
+        v, n = C.c_double(), C.c_uint32()
+        self.b.check(self.b.lib.pi_hip_last_kernel_us(self.b.ctx, C.byref(v), C.byref(n)))
+        return v.value, n.value
+
     def kv_write(self, layer, head, pos0, k: np.ndarray, v: np.ndarray) -> None:
+        self._live()
         k = np.ascontiguousarray(k, np.float32)
         v = np.ascontiguousarray(v, np.float32)
         n = k.size // self.model.spec.head_dim
         self.b.check(self.b.lib.pi_hip_kv_write(self.b.ctx, layer, head, pos0, n, _ptr(k), _ptr(v)))
 
     def kv_read(self, layer, head, pos0, n):
+        self._live()
         dh = self.model.spec.head_dim
         k = np.empty(n * dh, np.float32)
         v = np.empty(n * dh, np.float32)
@@ -580,9 +634,11 @@ class HipEngine:
         return k.reshape(n, dh), v.reshape(n, dh)
 
     def kv_fill_normal(self, n: int, seed: int) -> None:
+        self._live()
         self.b.check(self.b.lib.pi_hip_kv_fill_normal(self.b.ctx, n, seed))
 
     def kv_set_tokens(self, ids) -> None:
+        self._live()
         ids = np.ascontiguousarray(ids, np.uint32)
         self.b.check(self.b.lib.pi_hip_kv_set_tokens(self.b.ctx, _ptr(ids) if ids.size else None, ids.size))
 

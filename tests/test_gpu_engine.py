@@ -34,6 +34,20 @@ def tiny(pih):
     return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000), seed=7)
 
 
+@pytest.fixture(scope="module")
+def gqa(pih):
+    """8 query heads over 2 KV heads (kh = h / group, model.rs:995) with RoPE
+    on the first 32 of 64 dimensions (model.rs:930, 953-979)."""
+    return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=512, n_ff=1024, n_head=8, n_vocab=1000, n_head_kv=2,
+                                         n_rot=32), seed=13)
+
+
+def _with_eos(pih, model, eos):
+    """The same weights with another end-of-generation id."""
+    import dataclasses
+    return pih.SynthModel(dataclasses.replace(model.spec, eos_ids=(eos,)), model.tensors)
+
+
 def _close(got, want, rtol=1e-3, atol=1e-4):
     err = np.abs(got - want) - (atol + rtol * np.abs(want))
     return float(err.max())
@@ -100,17 +114,22 @@ def test_tiny_generate_matches_oracle(pih, backend, oracle, tiny, n_prompt):
 
 
 def test_tiny_prefix_reuse(pih, backend, oracle, tiny):
-    """tests/prefix_cache.rs:27-63 invariants on the device engine."""
-    eng = pih.HipEngine(backend, tiny, n_ctx=256)
+    """tests/prefix_cache.rs:27-63 invariants on the device engine.  A context
+    holds one engine, so the fresh run comes first."""
     base = [(i * 13 + 5) % 997 for i in range(70)]
     ext = base + [(i * 7 + 1) % 991 for i in range(40)]
+    fresh = pih.HipEngine(backend, tiny, n_ctx=256)
+    ids2, st2 = fresh.generate(ext, 4)
+    assert st2["prefill_cached_tokens"] == 0
+    fresh_logits = fresh.logits()
+    eng = pih.HipEngine(backend, tiny, n_ctx=256)
+    with pytest.raises(RuntimeError):
+        fresh.generate(ext, 4)                        # replaced by the bind above
     eng.generate(base, 2)
     ids, st = eng.generate(ext, 4)
     assert st["prefill_cached_tokens"] == 64          # min(common 70, cached 70, 109) // 32 * 32
     assert st["prefill_cached_tokens"] + st["prefill_tokens"] == len(ext)
-    fresh = pih.HipEngine(backend, tiny, n_ctx=256)
-    ids2, st2 = fresh.generate(ext, 4)
-    assert ids == ids2 and st2["prefill_cached_tokens"] == 0
+    assert ids == ids2 and _bits_equal(eng.logits(), fresh_logits)
     ref_ids, _ = oracle.OracleEngine(tiny, n_ctx=256, threads=4).generate(ext, 4)
     assert ids == ref_ids
     # a manual forward invalidates reuse (model.rs:825-831)
@@ -135,6 +154,65 @@ def test_tiny_context_full_and_eog(pih, backend, oracle, tiny):
     assert got == want and st["stop"] == st_ref["stop"] == "context_full"
     with pytest.raises(pih.PiError):
         eng.forward([1], [50])
+
+
+@pytest.mark.parametrize("at", [0, 5, 20])
+def test_tiny_eog_matches_oracle(pih, backend, oracle, tiny, at):
+    """generate stops at an end-of-generation id the oracle actually samples
+    (model.rs:1305-1306): the same ids and stop reason, and the logits left
+    behind are those that produced the EOG, as in Engine::generate, although
+    the device may have launched later forwards before it read that id."""
+    prompt = [(i * 29 + 3) % 1000 for i in range(37)]
+    free, _ = oracle.OracleEngine(tiny, n_ctx=256, threads=4).generate(prompt, 40)
+    # an id at index `at` that does not occur earlier
+    idx = next(i for i in range(at, len(free)) if free[i] not in free[:i])
+    m = _with_eos(pih, tiny, free[idx])
+    eng = pih.HipEngine(backend, m, n_ctx=256)
+    ref = oracle.OracleEngine(m, n_ctx=256, threads=4)
+    got, st = eng.generate(prompt, 40)
+    want, st_ref = ref.generate(prompt, 40)
+    assert got == want == free[:idx]
+    assert st["stop"] == st_ref["stop"] == "eog"
+    assert _bits_equal(eng.logits(), ref.logits())
+    assert eng.argmax() == free[idx]
+    # the engine continues cleanly after an EOG stop
+    got2, _ = eng.generate(prompt + want, 3)
+    want2, _ = ref.generate(prompt + want, 3)
+    assert got2 == want2
+
+
+def test_gqa_forward_logits(pih, backend, oracle, gqa, engine_mode):
+    """Grouped-query attention and partial RoPE, batch-1 forwards: logits bit
+    for bit at every position."""
+    eng = pih.HipEngine(backend, gqa, n_ctx=128)
+    assert backend.persistent_active() == (engine_mode == "persistent")
+    ref = oracle.OracleEngine(gqa, n_ctx=128, threads=4)
+    ids = [(i * 53 + 9) % 1000 for i in range(70)]
+    for pos, tok in enumerate(ids):
+        eng.forward([tok], [pos], want_logits=True)
+        ref.forward([tok], [pos], want_logits=True)
+        assert _bits_equal(eng.logits(), ref.logits()), f"pos {pos}"
+
+
+def test_gqa_kv_rows_and_generate(pih, backend, oracle, gqa):
+    """KV rows of every (layer, kv head) after a batched chunk, then greedy
+    generate with a partial last chunk, against the oracle."""
+    eng = pih.HipEngine(backend, gqa, n_ctx=160)
+    ref = oracle.OracleEngine(gqa, n_ctx=160, threads=4)
+    ids = [(i * 7 + 2) % 1000 for i in range(40)]
+    eng.forward(ids, list(range(40)), want_logits=True)
+    ref.forward(ids, list(range(40)), want_logits=True)
+    assert _bits_equal(eng.logits(), ref.logits())
+    kr, vr = ref.kv()
+    for layer in range(gqa.spec.n_layer):
+        for h in range(gqa.spec.n_head_kv):
+            k, v = eng.kv_read(layer, h, 0, 40)
+            assert _bits_equal(k, kr[layer, h, :40]) and _bits_equal(v, vr[layer, h, :40]), (layer, h)
+    prompt = [(i * 31 + 4) % 1000 for i in range(45)]
+    got, st = eng.generate(prompt, 40)
+    want, st_ref = ref.generate(prompt, 40)
+    assert got == want and st["stop"] == st_ref["stop"]
+    assert _bits_equal(eng.logits(), ref.logits())
 
 
 def test_minicpm2b_first_64_greedy_ids(pih, backend, engine_mode):

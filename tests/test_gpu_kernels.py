@@ -93,6 +93,8 @@ CASES = [
     (Q4_0, 11, 2304),
     (Q8_0, 5, 64),
     (Q4_K, 1, 4096),
+    (Q4_0, 9, 288),         # row lengths that end in a partial 256-element
+    (Q8_0, 7, 480),         # row of the LDS activation (q8 chunk permutation)
 ]
 
 
@@ -154,6 +156,25 @@ def test_gemv_special_scales(pih, backend, oracle, t):
     fin = ~np.isnan(want)
     assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))
     backend.clear_weight_cache()
+
+
+@pytest.mark.parametrize("t,rows,k", [(Q4_K, 5760, 2304), (Q6_K, 29, 512), (Q4_0, 2304, 5760), (Q8_0, 7, 480)])
+def test_gemv_dev_one_launch_equals_q8_pass(pih, backend, oracle, t, rows, k):
+    """gemv_dev (Q8 of x in every workgroup's LDS, one launch) equals the
+    GEMV on the separately quantized activation and the oracle, bit for bit."""
+    w = _rows(pih, t, rows, k, 400 + t)
+    x = np.random.default_rng(rows + 3 * k).standard_normal(k).astype(np.float32)
+    dev = backend.upload(t, w, rows, k)
+    xd, y1, y2 = backend.to_device(x), backend.alloc(rows * 4), backend.alloc(rows * 4)
+    qd, dd, sd = backend.alloc(k), backend.alloc(k // 32 * 4), backend.alloc(k // 32 * 4)
+    backend.gemv_dev(dev, xd.ptr, y1.ptr)
+    backend.q8_quantize_dev(xd.ptr, k, 1, qd.ptr, dd.ptr, sd.ptr)
+    backend.gemv_q8_dev(dev, qd.ptr, dd.ptr, sd.ptr, y2.ptr)
+    backend.synchronize()
+    a, b = y1.to_host(np.float32), y2.to_host(np.float32)
+    want = oracle.Pool(8).matmul(t, w, pih.row_bytes(t, k), k, x, 1, rows, oracle.Act(x, k, 1))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(a.view(np.uint32), want.view(np.uint32))
 
 
 def test_gemv_config2_head(pih, backend, oracle):

@@ -26,6 +26,15 @@ def tiny(pih):
     return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=256, n_ff=512, n_head=4, n_vocab=1000), seed=11)
 
 
+@pytest.fixture(scope="module")
+def gqa(pih):
+    """Grouped-query attention (8 query heads over 2 KV heads, model.rs:995
+    kh = h / group) with RoPE on the first 32 of 64 dimensions (n_rot,
+    model.rs:930, 953-979)."""
+    return pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=512, n_ff=1024, n_head=8, n_vocab=1000, n_head_kv=2,
+                                         n_rot=32), seed=13)
+
+
 def _deq(oracle, entry):
     t, ne0, ne1, buf = entry
     if t == 0:
@@ -65,6 +74,10 @@ class NumpyModel:
         v = v.reshape(-1, dh).copy()
         inv = s.rope_theta ** (-2.0 * np.arange(half) / s.n_rot)
         c, sn = np.cos(pos * inv), np.sin(pos * inv)
+        if self.mutate == "rope_all_dims":
+            half = dh // 2
+            inv = s.rope_theta ** (-2.0 * np.arange(half) / dh)
+            c, sn = np.cos(pos * inv), np.sin(pos * inv)
         if self.mutate == "neox_pairs":
             i0, i1 = np.arange(half), np.arange(half) + half
         else:
@@ -90,9 +103,10 @@ class NumpyModel:
             scale = 1.0 if self.mutate == "no_scale" else 1.0 / np.sqrt(dh)
             o = np.empty((s.n_head, dh))
             for h in range(s.n_head):
-                sc = K[h // group] @ q[h] * scale
+                kh = h % s.n_head_kv if self.mutate == "kv_head_mod" else h // group
+                sc = K[kh] @ q[h] * scale
                 e = np.exp(sc - sc.max())
-                o[h] = (e / e.sum()) @ V[h // group]
+                o[h] = (e / e.sum()) @ V[kh]
             proj = L["attn_output"] @ o.reshape(-1)
             x = proj if self.mutate == "no_residual" else x + proj
             xn = self._norm(x, L["ffn_norm"])
@@ -130,6 +144,23 @@ def test_forward_matches_float64_model(oracle, tiny):
 def test_planted_mistakes_are_caught(oracle, tiny, mutate):
     got = _oracle_logits(oracle, tiny, IDS)
     m = NumpyModel(oracle, tiny, mutate)
+    want = [m.step(t, p) for p, t in enumerate(IDS)]
+    assert _max_rel(got, want) > 1e-3, mutate
+
+
+def test_gqa_partial_rope_forward_matches_float64_model(oracle, gqa):
+    got = _oracle_logits(oracle, gqa, IDS)
+    m = NumpyModel(oracle, gqa)
+    want = [m.step(t, p) for p, t in enumerate(IDS)]
+    assert _max_rel(got, want) < 1e-4
+
+
+@pytest.mark.parametrize("mutate", ["kv_head_mod", "rope_all_dims", "neox_pairs"])
+def test_gqa_planted_mistakes_are_caught(oracle, gqa, mutate):
+    """Query head h must read KV head h / group (not h mod n_kv), and only
+    the first n_rot dimensions rotate."""
+    got = _oracle_logits(oracle, gqa, IDS)
+    m = NumpyModel(oracle, gqa, mutate)
     want = [m.step(t, p) for p, t in enumerate(IDS)]
     assert _max_rel(got, want) > 1e-3, mutate
 
