@@ -75,6 +75,19 @@ int         pi_hip_matvec(pi_ctx *ctx, uint32_t ggml_type, const uint8_t *w, siz
 /* OpenClBackend::clear_weight_cache (opencl.rs:385-389). */
 void        pi_hip_clear_weight_cache(pi_ctx *ctx);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, hosts that
+ * forbid hipMalloc): out[rows] = W x for a tensor already uploaded with
+ * pi_hip_upload, x (k floats) and out (rows floats) in host memory, with the
+ * same results as pi_hip_matvec.  It allocates nothing: x and y are staged
+ * in a static device array of (PI_NOALLOC_MAX_K + PI_NOALLOC_MAX_ROWS) * 4
+ * bytes per GPU, held until the process ends; larger tensors are rejected
+ * with PI_E_INVALID.  Every call on one GPU shares that array, so calls that
+ * overlap on one GPU (from several contexts or threads) race.  Synchronous. */
+#define PI_NOALLOC_MAX_K    16384u
+#define PI_NOALLOC_MAX_ROWS 262144u
+int         pi_hip_matvec_noalloc(pi_ctx *ctx, const pi_tensor *w, const float *x, float *out);
+
 /* ---------------------------------------------------------------------------
  * Explicit upload and device-pointer GEMV (no counterpart call in the
  * reference; it replaces the implicit upload inside matvec, opencl.rs:439-460).

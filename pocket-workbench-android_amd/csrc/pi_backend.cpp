@@ -1,9 +1,10 @@
 // C ABI of the pocketinfer MI355X backend: the OpenClBackend twin
 // (backend/opencl.rs), explicit upload, test hooks and the device-resident
 // engine (model.rs:678-1352).  Host code only; kernels are in pi_kernels.hip.
-#include <hip/hip_runtime_api.h>
+#include <hip/hip_runtime.h>
 
 #include <atomic>
+#include <mutex>
 #include <chrono>
 #include <cmath>
 #include <cstdarg>
@@ -25,6 +26,35 @@ struct pi_tensor {
     pi_layout L;
     uint8_t *dev = nullptr;
 };
+
+// Staging memory of pi_hip_matvec_noalloc: x (PI_NOALLOC_MAX_K floats), then
+// y (PI_NOALLOC_MAX_ROWS floats).  One copy per GPU, held until the process
+// ends.  In host code `scratch` only names the symbol: kernels and copies use
+// the device address hipGetSymbolAddress returns for each device.
+constexpr size_t kScratchBytes = ((size_t)PI_NOALLOC_MAX_K + PI_NOALLOC_MAX_ROWS) * 4;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+hipError_t g_scratch_err[kMaxDevices] = {};
+bool g_scratch_done[kMaxDevices] = {};
+
+// Device address of this device's `scratch`, looked up once per device with
+// that device current (pi_hip_create); null when the lookup failed.
+void *scratch_init(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_done[device]) {
+        void *p = nullptr;
+        g_scratch_err[device] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[device] = g_scratch_err[device] == hipSuccess ? p : nullptr;
+        g_scratch_done[device] = true;
+    }
+    return g_scratch_ptr[device];
+}
+}  // namespace
 
 namespace {
 
@@ -112,6 +142,7 @@ struct pi_ctx {
     int32_t *io_s = nullptr;
     size_t cap_x = 0, cap_y = 0;
     int max_lds = 65536;      // LDS bytes a workgroup may use on this device
+    void *scratch = nullptr;  // this device's `scratch` (pi_hip_matvec_noalloc)
     Engine *eng = nullptr;
 };
 
@@ -729,6 +760,7 @@ int pi_hip_create(pi_ctx **out, int device) {
         return PI_E_HIP;
     }
     c->stream = c->own;
+    c->scratch = scratch_init(device);
     int lds = 0;
     if (hipDeviceGetAttribute(&lds, hipDeviceAttributeSharedMemPerBlockOptin, device) == hipSuccess && lds > 0)
         c->max_lds = lds;
@@ -985,6 +1017,29 @@ int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, si
     HIPC(c, hipMemcpyAsync(c->io_x, x, k * 4, hipMemcpyHostToDevice, c->stream));
     if ((r = enqueue_gemv_x(c, t, c->io_x, c->io_y))) return r;
     HIPC(c, hipMemcpyAsync(out, c->io_y, rows * 4, hipMemcpyDeviceToHost, c->stream));
+    HIPC(c, hipStreamSynchronize(c->stream));
+    return PI_OK;
+}
+
+int pi_hip_matvec_noalloc(pi_ctx *c, const pi_tensor *w, const float *x, float *out) {
+    if (!c || !w || !x || !out) return c ? fail(c, PI_E_INVALID, "invalid matvec_noalloc arguments") : PI_E_INVALID;
+    if (take_injected(c)) return PI_E_INJECTED;
+    const size_t k = w->L.k, rows = w->L.rows;
+    if (k > PI_NOALLOC_MAX_K || rows > PI_NOALLOC_MAX_ROWS)
+        return fail(c, PI_E_INVALID, "matvec_noalloc: %zu rows x %zu exceeds the static staging (%u rows, k %u)",
+                    rows, k, (unsigned)PI_NOALLOC_MAX_ROWS, (unsigned)PI_NOALLOC_MAX_K);
+    if (!c->scratch) {
+        const hipError_t e = (c->device >= 0 && c->device < kMaxDevices) ? g_scratch_err[c->device] : hipErrorInvalidDevice;
+        return fail(c, PI_E_HIP, "matvec_noalloc: no staging address for device %d: %s", c->device, hipGetErrorString(e));
+    }
+    if (pi_gemv_x_lds_bytes(w->L.type, w->L.g, w->L.k) > (size_t)c->max_lds)
+        return fail(c, PI_E_UNSUPPORTED, "matvec_noalloc: row length %zu does not fit the kernel's LDS", k);
+    float *xs = reinterpret_cast<float *>(c->scratch);
+    float *ys = xs + PI_NOALLOC_MAX_K;
+    HIPC(c, hipMemcpyAsync(xs, x, k * 4, hipMemcpyHostToDevice, c->stream));
+    const pi_matset M = make_set({{w, ys}});
+    HIPC(c, pi_launch_gemv_x(M, xs, gemv_blocks(w->L.ntiles), c->stream));
+    HIPC(c, hipMemcpyAsync(out, ys, rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
     return PI_OK;
 }

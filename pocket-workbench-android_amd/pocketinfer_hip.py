@@ -31,6 +31,7 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
 BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 PI_OK = 0
+PI_NOALLOC_MAX_K, PI_NOALLOC_MAX_ROWS = 16384, 262144   # pi_hip_matvec_noalloc limits (pocketinfer_hip.h)
 ERRORS = {-1: "PI_E_INVALID", -2: "PI_E_UNSUPPORTED", -3: "PI_E_HIP", -4: "PI_E_SELFTEST",
           -5: "PI_E_NOMEM", -6: "PI_E_INJECTED", -7: "PI_E_STOPPED", -8: "PI_E_CONTEXT_FULL",
           -9: "PI_E_NOMODEL"}
@@ -38,7 +39,7 @@ ERRORS = {-1: "PI_E_INVALID", -2: "PI_E_UNSUPPORTED", -3: "PI_E_HIP", -4: "PI_E_
 # Every exported symbol of include/pocketinfer_hip.h.
 EXPORTS = [
     "pi_hip_probe", "pi_hip_create", "pi_hip_destroy", "pi_hip_name", "pi_last_error",
-    "pi_hip_supports", "pi_hip_selftest", "pi_hip_matvec", "pi_hip_clear_weight_cache",
+    "pi_hip_supports", "pi_hip_selftest", "pi_hip_matvec", "pi_hip_clear_weight_cache", "pi_hip_matvec_noalloc",
     "pi_hip_upload", "pi_hip_tensor_free", "pi_hip_tensor_bytes", "pi_hip_gemv_dev",
     "pi_hip_gemv_q8_dev", "pi_hip_time_gemv", "pi_hip_q8_quantize_dev", "pi_hip_dev_alloc",
     "pi_hip_dev_free", "pi_hip_copy_h2d", "pi_hip_copy_d2h", "pi_hip_copy_d2d", "pi_hip_set_stream", "pi_hip_synchronize",
@@ -110,6 +111,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_hip_selftest": (i32, [vp]),
         "pi_hip_matvec": (i32, [vp, u32, vp, sz, sz, vp, vp, sz]),
         "pi_hip_clear_weight_cache": (None, [vp]),
+        "pi_hip_matvec_noalloc": (i32, [vp, vp, vp, vp]),
         "pi_hip_upload": (i32, [vp, u32, vp, sz, sz, C.POINTER(vp)]),
         "pi_hip_tensor_free": (None, [vp, vp]),
         "pi_hip_tensor_bytes": (sz, [vp]),
@@ -320,6 +322,14 @@ class HipBackend:
         out = np.empty(rows, np.float32)
         self._keep.append(w)  # the upload cache is keyed by the host pointer (opencl.rs:439)
         self.check(self.lib.pi_hip_matvec(self.ctx, ggml_type, _ptr(w), w.nbytes, k, _ptr(x), _ptr(out), rows))
+        return out
+
+    def matvec_noalloc(self, w: "Tensor", x: np.ndarray) -> np.ndarray:
+        """W x for an uploaded tensor, staged through the library's static
+        device array (no device allocation; see pi_hip_matvec_noalloc)."""
+        x = np.ascontiguousarray(x, np.float32)
+        out = np.empty(w.rows, np.float32)
+        self.check(self.lib.pi_hip_matvec_noalloc(self.ctx, w.handle, _ptr(x), _ptr(out)))
         return out
 
     def clear_weight_cache(self) -> None:
