@@ -35,7 +35,7 @@ Also measured here:
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip SECTIONS]
        python bench.py --profile-gemv     (GEMV launches and a 256 MiB copy, for counter runs)
-       python bench.py --profile-decode   (one 32-token decode, for counter runs)
+       python bench.py --profile-decode   (one config-3 decode and a 256 MiB copy, for counter runs)
 """
 import argparse
 import json
@@ -134,6 +134,7 @@ def bench_long_context(b, model, n_fill, n_gen, wbytes):
     kern_us, kern_n = eng.last_kernel_us()
     b.time_kernels(False)
     tps = st["gen_tokens"] / (st["gen_ms"] / 1000.0)
+    trace = stage_breakdown(b, eng, 17, n_fill + n_gen, spec_heads(model), spec_kv(model))
     # forward j (1..n_gen-1) sits at position n_fill + j and reads positions 0..n_fill + j
     kv_bytes = KV_BYTES_PER_POS * (n_fill + 1 + n_gen / 2)
     per_tok = wbytes + kv_bytes
@@ -142,7 +143,50 @@ def bench_long_context(b, model, n_fill, n_gen, wbytes):
             "reused": st["prefill_cached_tokens"], "bytes_per_forward": round(per_tok),
             "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / per_tok, 1),
             "frac": round(tps * per_tok / (HBM_PEAK_GBS * 1e9), 4),
-            "kernel_gbs": round(per_tok / (kern_us * 1e-6) / 1e9, 1) if kern_us else None}
+            "kernel_gbs": round(per_tok / (kern_us * 1e-6) / 1e9, 1) if kern_us else None,
+            "attention_us_per_layer": trace["us_per_layer"]["attention"],
+            "attention_gbs": trace["attention_gbs"], "attention_frac": trace["attention_frac"],
+            "stage_trace": trace}
+
+
+def spec_heads(model):
+    return model.spec.n_head
+
+
+def spec_kv(model):
+    return model.spec.n_head_kv
+
+
+STAGES = ("qkv", "attention", "attn_output", "ffn_gate_up", "ffn_down")
+
+
+def stage_breakdown(b, eng, tok, pos, n_head=36, n_kv=36, dh=64):
+    """One traced forward of `tok` at `pos` on the persistent kernel: every
+    workgroup records the device clock (100 MHz) at the end of each stage.
+    A stage of layer l ends when its slowest workgroup ends it; its time runs
+    from the end of the previous stage.  Attention reads (and writes) the K
+    and V rows of positions 0..pos of every KV head: 2 * n_kv * (pos+1) * dh
+    * 4 bytes per layer."""
+    b.stage_trace(True)
+    eng.forward([tok], [pos], want_logits=True)
+    tr = b.stage_trace_read().astype("int64")
+    b.stage_trace(False)
+    n_layer = (tr.shape[1] - 4 - 32) // 5
+    end = tr.max(axis=0)                                  # slowest workgroup per slot
+    per = {k: [] for k in STAGES}
+    for l in range(n_layer):
+        prev = end[1] if l == 0 else end[6 + 5 * (l - 1)]
+        for i, k in enumerate(STAGES):
+            cur = end[2 + 5 * l + i]
+            per[k].append((cur - prev) / 100.0)           # us
+            prev = cur
+    mean = {k: round(float(sum(v) / len(v)), 2) for k, v in per.items()}
+    kv_layer = 2 * n_kv * (pos + 1) * dh * 4
+    total = (end[2 + 5 * n_layer] - end[0]) / 100.0
+    return {"position": pos, "us_per_layer": mean, "layers": n_layer, "forward_us": round(float(total), 1),
+            "attention_kv_bytes_per_layer": kv_layer,
+            "attention_gbs": round(kv_layer / (mean["attention"] * 1e-6) / 1e9, 1),
+            "attention_frac": round(kv_layer / (mean["attention"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def profile_gemv(b):
@@ -158,10 +202,11 @@ def profile_gemv(b):
 
 
 def profile_decode(b, model, prompt):
-    """One 32-token decode of the config-3 model and one 256 MiB device copy:
-    a short program for rocprofv3 counter runs on k_mega."""
-    eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + 40)
-    ids, st = eng.generate(prompt, 32)
+    """One config-3 decode (128-id prompt, 256 tokens: k_mega at positions
+    128..382) and one 256 MiB device copy: a short program for rocprofv3
+    counter runs on k_mega."""
+    eng = pih.HipEngine(b, model, n_ctx=N_PROMPT + N_GEN + 8)
+    ids, st = eng.generate(prompt, N_GEN)
     n = 256 << 20
     src, dst = b.alloc(n), b.alloc(n)
     b.copy_d2d(dst, src, n)
@@ -277,6 +322,9 @@ def run(args, skip, steps, warmup, b, t_start):
                     if g["prompt"] == prompt and g["model_seed"] == MODEL_SEED and len(ids) >= g["n_gen"]:
                         match = ids[: g["n_gen"]] == g["gen_ids"]
         b.time_kernels(False)
+    trace = stage_breakdown(b, eng, 17, N_PROMPT + N_GEN - 1) if eng is not None else None
+    if trace:
+        log(f"stage trace: {trace}")
     gen_tokens = sum(st["gen_tokens"] for st in runs)
     gen_ms = sum(st["gen_ms"] for st in runs)
     fwd = sum(max(st["gen_tokens"] - 1, 0) for st in runs)
@@ -331,6 +379,7 @@ def run(args, skip, steps, warmup, b, t_start):
         "decode_weight_roofline": {"weight_bytes_per_token": wbytes,
                                    "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
                                    "frac": round(tps * wbytes / (HBM_PEAK_GBS * 1e9), 4)},
+        "decode_stage_trace": trace,
         "greedy_first_64_match_oracle": match,
         "prefill": prefill,
         "long_context": long_ctx,

@@ -190,7 +190,7 @@ typedef struct {              /* Config (model.rs:14-29) + tensors */
     const pi_layer_desc *layers;
 } pi_model_desc;
 
-typedef struct {              /* GenOpts (model.rs:657-664); greedy only: temp <= 0 */
+typedef struct {              /* GenOpts (model.rs:657-664): temp <= 0 is greedy */
     uint32_t max_tokens;
     float    temp, top_p;
     uint64_t seed;
@@ -213,8 +213,12 @@ int  pi_hip_forward(pi_ctx *ctx, const uint32_t *ids, const int32_t *pos, int b,
 int  pi_hip_logits(pi_ctx *ctx, float *out, size_t n);
 /* Greedy sample (sampler.rs:26-36) on the device: first index of the max. */
 int  pi_hip_argmax(pi_ctx *ctx, uint32_t *id);
-/* Engine::generate (model.rs:1235-1352), greedy: 32-token prefill chunks with
- * the reference reuse rule (1258-1268), n tokens for n-1 forwards, is_eog stop. */
+/* Engine::generate (model.rs:1235-1352): 32-token prefill chunks with the
+ * reference reuse rule (1258-1268), n tokens for n-1 forwards, is_eog stop.
+ * temp <= 0 is greedy and stays on the device; temp > 0 draws each token with
+ * sample() (sampler.rs:21-92, seeded with opts->seed) on the host from the
+ * logits of the last forward, and leaves the last draw's weights in the
+ * logits, as the reference's sample() does. */
 int  pi_hip_generate(pi_ctx *ctx, const uint32_t *prompt, size_t n, const pi_genopts *opts,
                      pi_genstats *stats, uint32_t *gen_ids);
 /* Direct KV access (KvCache is pub, model.rs:352-359): rows for positions
@@ -265,6 +269,20 @@ int  pi_hip_last_decode_us(pi_ctx *ctx, double *per_token_us);
  * one forward's kernels over the n forwards of the last generate call. */
 int  pi_hip_time_kernels(pi_ctx *ctx, int enable);
 int  pi_hip_last_kernel_us(pi_ctx *ctx, double *per_forward_us, uint32_t *n);
+
+/* ---------------------------------------------------------------------------
+ * Sampling (sampler.rs), host-side.
+ * ------------------------------------------------------------------------- */
+/* Rng::new (sampler.rs:6-8): the SplitMix64 state for a seed. */
+uint64_t pi_rng_new(uint64_t seed);
+/* Rng::next_u64 (sampler.rs:9-15): advances *state. */
+uint64_t pi_rng_next_u64(uint64_t *state);
+/* sample (sampler.rs:21-92): greedy for temp <= 0, else temperature and
+ * top-p over n logits (overwritten with the weights, as the reference's
+ * &mut [f32] is), drawing from *rng_state.  Equal weights are ordered by
+ * index in the top-p cut (the reference's sort_unstable_by leaves them in an
+ * unspecified order). */
+uint32_t pi_sample(float *logits, size_t n, float temp, float top_p, uint64_t *rng_state);
 
 /* ---------------------------------------------------------------------------
  * Seeded synthetic data (host-side, deterministic across machines: integer

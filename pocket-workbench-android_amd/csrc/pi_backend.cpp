@@ -21,6 +21,7 @@
 #include "pi_kernels.h"
 #include "pi_mega.h"
 #include "pi_prefill.h"
+#include "pi_sample.h"
 
 struct pi_tensor {
     pi_layout L;
@@ -1368,6 +1369,71 @@ int pi_hip_last_kernel_us(pi_ctx *c, double *us, uint32_t *n) {
     return PI_OK;
 }
 
+// Decode with temperature / top-p sampling (model.rs:1299-1337 with
+// sampler.rs:21-92): after every forward the logits come back to the host,
+// where the token is drawn from the seeded generator; the token then feeds
+// the next forward.  The logits left on the device afterwards are the
+// weights the last draw used, as sample() leaves them in the reference's
+// scratch.logits.
+static int sample_decode(pi_ctx *c, Engine &e, size_t n, const pi_genopts *o, pi_genstats *st, uint32_t *gen_ids,
+                         bool mega) {
+    int r;
+    auto g0 = std::chrono::steady_clock::now();
+    pi_rng rng = pi_rng_make(o->seed);
+    std::vector<float> lg(e.n_vocab);
+    std::vector<uint32_t> idx;
+    hipEvent_t ka = nullptr, kb = nullptr;
+    if (c->time_kernels) {
+        HIPC(c, hipEventCreate(&ka));
+        HIPC(c, hipEventCreate(&kb));
+    }
+    double kern_ms = 0.0;
+    size_t fwd = 0;
+    const size_t max_gen = o->max_tokens;
+    for (size_t i = 0; i < max_gen; i++) {
+        if (c->stop.load()) { snprintf(st->stop, sizeof st->stop, "user_stop"); break; }
+        HIPC(c, hipMemcpyAsync(lg.data(), e.logits, (size_t)e.n_vocab * 4, hipMemcpyDeviceToHost, c->stream));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        const uint32_t tok = pi_sample_logits(lg.data(), lg.size(), o->temp, o->top_p, rng, idx);
+        bool eog = false;
+        for (uint32_t x : e.eos) eog |= (x == tok);
+        if (eog) { snprintf(st->stop, sizeof st->stop, "eog"); break; }
+        gen_ids[st->gen_tokens++] = tok;
+        if (i + 1 == max_gen) break;
+        const size_t pos = n + i;
+        if (pos >= e.n_ctx) { snprintf(st->stop, sizeof st->stop, "context_full"); break; }
+        if (ka) HIPC(c, hipEventRecord(ka, c->stream));
+        if (mega) {
+            HIPC(c, mega_token(c, e, (int32_t)pos, tok, nullptr, nullptr, true, true));
+        } else {
+            if ((r = set_state(c, e, (int32_t)pos, tok, 0, 0))) return r;
+            HIPC(c, enqueue_step(e, PI_STEP_EMBED, nullptr, c->stream));
+            HIPC(c, run_step(c, e, STEP_DECODE));
+        }
+        if (kb) HIPC(c, hipEventRecord(kb, c->stream));
+        HIPC(c, hipStreamSynchronize(c->stream));
+        if ((r = mega_check(c, e))) { e.kv_tokens.clear(); e.cached_prefill_len = 0; return r; }
+        if (ka) {
+            float ms = 0.f;
+            HIPC(c, hipEventElapsedTime(&ms, ka, kb));
+            kern_ms += ms;
+        }
+        e.kv_tokens.push_back(tok);
+        fwd++;
+    }
+    // the weights of the last draw stay in the logits, as in the reference
+    if (st->gen_tokens || strcmp(st->stop, "eog") == 0)
+        HIPC(c, hipMemcpy(e.logits, lg.data(), (size_t)e.n_vocab * 4, hipMemcpyHostToDevice));
+    if (ka) (void)hipEventDestroy(ka);
+    if (kb) (void)hipEventDestroy(kb);
+    e.last_kernel_us = (c->time_kernels && fwd) ? kern_ms * 1000.0 / (double)fwd : 0.0;
+    e.last_kernel_n = c->time_kernels ? (uint32_t)fwd : 0u;
+    if (strcmp(st->stop, "user_stop") == 0) { e.kv_tokens.clear(); e.cached_prefill_len = 0; }
+    st->gen_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - g0).count();
+    e.last_decode_us = fwd ? st->gen_ms * 1000.0 / (double)fwd : 0.0;
+    return PI_OK;
+}
+
 int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopts *o, pi_genstats *st,
                     uint32_t *gen_ids) {
     if (!c || !o || !st) return PI_E_INVALID;
@@ -1376,7 +1442,7 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     memset(st, 0, sizeof *st);
     snprintf(st->stop, sizeof st->stop, "max_tokens");
     if (n == 0 || !prompt) return fail(c, PI_E_INVALID, "empty prompt");
-    if (o->temp > 0.0f) return fail(c, PI_E_UNSUPPORTED, "only greedy decoding (temp <= 0) runs on the device");
+    if (!(o->temp == o->temp) || !(o->top_p == o->top_p)) return fail(c, PI_E_INVALID, "temp / top_p is NaN");
     if (o->max_tokens > 0 && !gen_ids) return fail(c, PI_E_INVALID, "gen_ids is null");
     if (take_injected(c)) return PI_E_INJECTED;
     for (size_t i = 0; i < n; i++)
@@ -1475,6 +1541,7 @@ prefill_done:
     st->prefill_tokens = (uint32_t)(off - reused);
     st->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     e->cached_prefill_len = n;
+    if (o->temp > 0.0f) return sample_decode(c, *e, n, o, st, gen_ids, mega);
     // Decode: n tokens take n-1 forwards (model.rs:1299-1337).
     auto g0 = std::chrono::steady_clock::now();
     hipEvent_t ea, eb;
@@ -1581,6 +1648,25 @@ prefill_done:
     if (strcmp(st->stop, "user_stop") == 0) { e->kv_tokens.clear(); e->cached_prefill_len = 0; }
     st->gen_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - g0).count();
     return PI_OK;
+}
+
+uint64_t pi_rng_new(uint64_t seed) { return pi_rng_make(seed).s; }
+
+uint64_t pi_rng_next_u64(uint64_t *state) {
+    if (!state) return 0;
+    pi_rng r{*state};
+    const uint64_t v = pi_rng_u64(r);
+    *state = r.s;
+    return v;
+}
+
+uint32_t pi_sample(float *logits, size_t n, float temp, float top_p, uint64_t *rng_state) {
+    if (!logits || !rng_state) return 0;
+    pi_rng r{*rng_state};
+    std::vector<uint32_t> idx;
+    const uint32_t tok = pi_sample_logits(logits, n, temp, top_p, r, idx);
+    *rng_state = r.s;
+    return tok;
 }
 
 int pi_hip_kv_write(pi_ctx *c, uint32_t layer, uint32_t h, uint32_t pos0, uint32_t n, const float *k, const float *v) {

@@ -50,7 +50,7 @@ EXPORTS = [
     "pi_hip_time_kernels", "pi_hip_last_kernel_us", "pi_hip_time_gemv_x",
     "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
     "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor", "pi_synth_kv_normal",
-    "pi_quantize_row",
+    "pi_quantize_row", "pi_rng_new", "pi_rng_next_u64", "pi_sample",
 ]
 
 
@@ -156,6 +156,9 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_synth_kv_normal": (i32, [u64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
         "pi_synth_tensor": (i32, [u64, u32, sz, sz, f32, f32, vp, i32]),
         "pi_quantize_row": (i32, [u32, vp, sz, vp]),
+        "pi_rng_new": (u64, [u64]),
+        "pi_rng_next_u64": (u64, [C.POINTER(u64)]),
+        "pi_sample": (u32, [vp, sz, f32, f32, C.POINTER(u64)]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -227,6 +230,23 @@ def quantize_row(t: int, x: np.ndarray) -> np.ndarray:
     out = np.empty(row_bytes(t, x.size), np.uint8)
     _check(load_library().pi_quantize_row(t, _ptr(x), x.size, _ptr(out)), None)
     return out
+
+
+class Rng:
+    """sampler.rs:1-20 (SplitMix64) over the library's host sampler."""
+
+    def __init__(self, seed: int):
+        self.state = C.c_uint64(load_library().pi_rng_new(seed))
+
+    def next_u64(self) -> int:
+        return load_library().pi_rng_next_u64(C.byref(self.state))
+
+
+def sample(logits: np.ndarray, temp: float, top_p: float, rng: Rng) -> int:
+    """sample() (sampler.rs:21-92) on a float32 array, overwritten like the
+    reference's &mut [f32]."""
+    assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"]
+    return load_library().pi_sample(_ptr(logits), logits.size, temp, top_p, C.byref(rng.state))
 
 
 def _check(rc: int, ctx) -> None:

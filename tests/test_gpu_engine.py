@@ -181,6 +181,24 @@ def test_tiny_eog_matches_oracle(pih, backend, oracle, tiny, at):
     assert got2 == want2
 
 
+@pytest.mark.parametrize("temp,top_p,n_prompt", [(0.7, 0.95, 37), (1.0, 1.0, 1), (0.4, 0.5, 64)])
+def test_tiny_sampled_generate_matches_oracle(pih, backend, oracle, tiny, temp, top_p, n_prompt):
+    """Temperature / top-p generate (the app's temp 0.7, top_p 0.95 and seed
+    0xC0FFEE, jni.rs:459-466): the same ids and stop as the oracle's generate,
+    and the same weights left in the logits (sampler.rs:21-92)."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=256)
+    ref = oracle.OracleEngine(tiny, n_ctx=256, threads=4)
+    prompt = [(i * 41 + 7) % 1000 for i in range(n_prompt)]
+    got, st = eng.generate(prompt, 40, temp=temp, top_p=top_p, seed=0xC0FFEE)
+    want, st_ref = ref.generate(prompt, 40, temp=temp, top_p=top_p, seed=0xC0FFEE)
+    assert got == want and st["stop"] == st_ref["stop"]
+    assert _bits_equal(eng.logits(), ref.logits())
+    # greedy afterwards is unaffected by the sampled run
+    g1, _ = eng.generate(prompt, 8)
+    g2, _ = ref.generate(prompt, 8)
+    assert g1 == g2
+
+
 def test_gqa_forward_logits(pih, backend, oracle, gqa, engine_mode):
     """Grouped-query attention and partial RoPE, batch-1 forwards: logits bit
     for bit at every position."""
