@@ -271,6 +271,51 @@ int  pi_hip_time_kernels(pi_ctx *ctx, int enable);
 int  pi_hip_last_kernel_us(pi_ctx *ctx, double *per_forward_us, uint32_t *n);
 
 /* ---------------------------------------------------------------------------
+ * GGUF reader (gguf.rs), host-side.  The file is mapped read-only; tensor
+ * data and the model descriptor point into the mapping, which stays valid
+ * until pi_gguf_close.  Errors copy a message into err (err_len bytes).
+ * ------------------------------------------------------------------------- */
+typedef struct pi_gguf pi_gguf;
+/* Gguf::load (gguf.rs:113-192): MappedFile::open (util.rs:163-192) + parse
+ * of a GGUF v2/v3 header, metadata and tensor table. */
+int         pi_gguf_open(const char *path, pi_gguf **out, char *err, size_t err_len);
+/* Gguf::parse over bytes the caller keeps alive (no copy). */
+int         pi_gguf_parse(const void *bytes, size_t len, pi_gguf **out, char *err, size_t err_len);
+void        pi_gguf_close(pi_gguf *g);
+uint32_t    pi_gguf_version(const pi_gguf *g);
+/* Gguf::data_offset: start of the tensor data (aligned to general.alignment). */
+uint64_t    pi_gguf_data_offset(const pi_gguf *g);
+/* Gguf::keys (gguf.rs:198-200): metadata keys in file order. */
+size_t      pi_gguf_n_kv(const pi_gguf *g);
+const char *pi_gguf_key(const pi_gguf *g, size_t i);
+/* The GGUF value type of a key (0 U8 ... 12 F64). */
+int         pi_gguf_kv_type(const pi_gguf *g, const char *key, uint32_t *type);
+/* Gguf::get_u64 / get_f32 / get_bool / get_str (gguf.rs:206-255). */
+int         pi_gguf_get_u64(const pi_gguf *g, const char *key, uint64_t *v);
+int         pi_gguf_get_f32(const pi_gguf *g, const char *key, float *v);
+int         pi_gguf_get_bool(const pi_gguf *g, const char *key, int *v);
+int         pi_gguf_get_str(const pi_gguf *g, const char *key, const char **s, size_t *len);
+/* Gguf::array_len / array_type / array_strings / array_i32 / array_f32
+ * (gguf.rs:257-316). */
+int         pi_gguf_array_info(const pi_gguf *g, const char *key, uint32_t *etype, uint64_t *count);
+int         pi_gguf_array_str(const pi_gguf *g, const char *key, uint64_t i, const char **s, size_t *len);
+int         pi_gguf_array_i32(const pi_gguf *g, const char *key, int32_t *out, size_t n);
+int         pi_gguf_array_f32(const pi_gguf *g, const char *key, float *out, size_t n);
+/* Gguf::tensors / tensor / tensor_data (gguf.rs:318-336). */
+size_t      pi_gguf_n_tensors(const pi_gguf *g);
+int64_t     pi_gguf_find_tensor(const pi_gguf *g, const char *name);
+int         pi_gguf_tensor_info(const pi_gguf *g, size_t i, const char **name, uint32_t *type, uint32_t *n_dims,
+                                uint64_t ne[4], uint64_t *offset);
+int         pi_gguf_tensor_data(const pi_gguf *g, size_t i, const void **data, size_t *nbytes, char *err,
+                                size_t err_len);
+/* Config::from_gguf (model.rs:31-97) and Model::load's tensor binding and
+ * shape checks (model.rs:487-601), with the tokenizer's vocabulary size and
+ * end-of-generation ids (tokenizer.rs:41-109): fills *m for
+ * pi_hip_model_bind.  layers holds max_layers entries, eos max_eos ids. */
+int         pi_gguf_model_desc(const pi_gguf *g, pi_model_desc *m, pi_layer_desc *layers, uint32_t max_layers,
+                               uint32_t *eos, uint32_t max_eos, char *err, size_t err_len);
+
+/* ---------------------------------------------------------------------------
  * Sampling (sampler.rs), host-side.
  * ------------------------------------------------------------------------- */
 /* Rng::new (sampler.rs:6-8): the SplitMix64 state for a seed. */

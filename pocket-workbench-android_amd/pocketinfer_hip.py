@@ -51,6 +51,10 @@ EXPORTS = [
     "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
     "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor", "pi_synth_kv_normal",
     "pi_quantize_row", "pi_rng_new", "pi_rng_next_u64", "pi_sample",
+    "pi_gguf_open", "pi_gguf_parse", "pi_gguf_close", "pi_gguf_version", "pi_gguf_data_offset", "pi_gguf_n_kv",
+    "pi_gguf_key", "pi_gguf_kv_type", "pi_gguf_get_u64", "pi_gguf_get_f32", "pi_gguf_get_bool", "pi_gguf_get_str",
+    "pi_gguf_array_info", "pi_gguf_array_str", "pi_gguf_array_i32", "pi_gguf_array_f32", "pi_gguf_n_tensors",
+    "pi_gguf_find_tensor", "pi_gguf_tensor_info", "pi_gguf_tensor_data", "pi_gguf_model_desc",
 ]
 
 
@@ -156,6 +160,28 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_synth_kv_normal": (i32, [u64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
         "pi_synth_tensor": (i32, [u64, u32, sz, sz, f32, f32, vp, i32]),
         "pi_quantize_row": (i32, [u32, vp, sz, vp]),
+        "pi_gguf_open": (i32, [C.c_char_p, C.POINTER(vp), C.c_char_p, sz]),
+        "pi_gguf_parse": (i32, [vp, sz, C.POINTER(vp), C.c_char_p, sz]),
+        "pi_gguf_close": (None, [vp]),
+        "pi_gguf_version": (u32, [vp]),
+        "pi_gguf_data_offset": (u64, [vp]),
+        "pi_gguf_n_kv": (sz, [vp]),
+        "pi_gguf_key": (C.c_char_p, [vp, sz]),
+        "pi_gguf_kv_type": (i32, [vp, C.c_char_p, C.POINTER(u32)]),
+        "pi_gguf_get_u64": (i32, [vp, C.c_char_p, C.POINTER(u64)]),
+        "pi_gguf_get_f32": (i32, [vp, C.c_char_p, C.POINTER(f32)]),
+        "pi_gguf_get_bool": (i32, [vp, C.c_char_p, C.POINTER(i32)]),
+        "pi_gguf_get_str": (i32, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)]),
+        "pi_gguf_array_info": (i32, [vp, C.c_char_p, C.POINTER(u32), C.POINTER(u64)]),
+        "pi_gguf_array_str": (i32, [vp, C.c_char_p, u64, C.POINTER(vp), C.POINTER(sz)]),
+        "pi_gguf_array_i32": (i32, [vp, C.c_char_p, vp, sz]),
+        "pi_gguf_array_f32": (i32, [vp, C.c_char_p, vp, sz]),
+        "pi_gguf_n_tensors": (sz, [vp]),
+        "pi_gguf_find_tensor": (C.c_int64, [vp, C.c_char_p]),
+        "pi_gguf_tensor_info": (i32, [vp, sz, C.POINTER(C.c_char_p), C.POINTER(u32), C.POINTER(u32),
+                                      C.POINTER(u64), C.POINTER(u64)]),
+        "pi_gguf_tensor_data": (i32, [vp, sz, C.POINTER(vp), C.POINTER(sz), C.c_char_p, sz]),
+        "pi_gguf_model_desc": (i32, [vp, C.POINTER(ModelDesc), vp, u32, vp, u32, C.c_char_p, sz]),
         "pi_rng_new": (u64, [u64]),
         "pi_rng_next_u64": (u64, [C.POINTER(u64)]),
         "pi_sample": (u32, [vp, sz, f32, f32, C.POINTER(u64)]),
@@ -572,6 +598,140 @@ def synth_model(spec: ModelSpec, seed: int = 1234, threads: int | None = None) -
     return m
 
 
+class Gguf:
+    """Gguf (gguf.rs:31-336) over the library's reader: the file stays mapped
+    read-only until close(); tensor data are numpy views of the mapping."""
+
+    def __init__(self, path: str | None = None, data: bytes | None = None):
+        L = load_library()
+        h, err = C.c_void_p(), C.create_string_buffer(512)
+        if data is not None:
+            self._buf = C.create_string_buffer(bytes(data), len(data))   # kept alive: no copy in the library
+            rc = L.pi_gguf_parse(self._buf, len(data), C.byref(h), err, 512)
+        else:
+            rc = L.pi_gguf_open(str(path).encode(), C.byref(h), err, 512)
+        if rc != PI_OK:
+            raise PiError(rc, err.value.decode())
+        self.h = h.value
+
+    # -- header and metadata -------------------------------------------------
+    @property
+    def version(self) -> int:
+        return load_library().pi_gguf_version(self.h)
+
+    @property
+    def data_offset(self) -> int:
+        return load_library().pi_gguf_data_offset(self.h)
+
+    def keys(self) -> list:
+        L = load_library()
+        return [L.pi_gguf_key(self.h, i).decode() for i in range(L.pi_gguf_n_kv(self.h))]
+
+    def kv_type(self, key: str) -> int | None:
+        t = C.c_uint32()
+        return t.value if load_library().pi_gguf_kv_type(self.h, key.encode(), C.byref(t)) == PI_OK else None
+
+    def get_u64(self, key: str) -> int | None:
+        v = C.c_uint64()
+        return v.value if load_library().pi_gguf_get_u64(self.h, key.encode(), C.byref(v)) == PI_OK else None
+
+    def get_f32(self, key: str) -> float | None:
+        v = C.c_float()
+        return v.value if load_library().pi_gguf_get_f32(self.h, key.encode(), C.byref(v)) == PI_OK else None
+
+    def get_bool(self, key: str) -> bool | None:
+        v = C.c_int()
+        return bool(v.value) if load_library().pi_gguf_get_bool(self.h, key.encode(), C.byref(v)) == PI_OK else None
+
+    def get_str(self, key: str) -> bytes | None:
+        p, n = C.c_void_p(), C.c_size_t()
+        if load_library().pi_gguf_get_str(self.h, key.encode(), C.byref(p), C.byref(n)) != PI_OK:
+            return None
+        return C.string_at(p.value, n.value) if n.value else b""
+
+    def array_info(self, key: str):
+        et, n = C.c_uint32(), C.c_uint64()
+        if load_library().pi_gguf_array_info(self.h, key.encode(), C.byref(et), C.byref(n)) != PI_OK:
+            return None
+        return et.value, n.value
+
+    def array_strings(self, key: str) -> list:
+        info = self.array_info(key)
+        if info is None:
+            raise KeyError(key)
+        out = []
+        for i in range(info[1]):
+            p, n = C.c_void_p(), C.c_size_t()
+            _check(load_library().pi_gguf_array_str(self.h, key.encode(), i, C.byref(p), C.byref(n)), None)
+            out.append(C.string_at(p.value, n.value) if n.value else b"")
+        return out
+
+    def array_i32(self, key: str) -> np.ndarray:
+        info = self.array_info(key)
+        out = np.empty(info[1] if info else 0, np.int32)
+        _check(load_library().pi_gguf_array_i32(self.h, key.encode(), _ptr(out) if out.size else None, out.size), None)
+        return out
+
+    def array_f32(self, key: str) -> np.ndarray:
+        info = self.array_info(key)
+        out = np.empty(info[1] if info else 0, np.float32)
+        _check(load_library().pi_gguf_array_f32(self.h, key.encode(), _ptr(out) if out.size else None, out.size), None)
+        return out
+
+    # -- tensors -----------------------------------------------------------------
+    def n_tensors(self) -> int:
+        return load_library().pi_gguf_n_tensors(self.h)
+
+    def tensor_info(self, i: int) -> dict:
+        name, t, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        ne, off = (C.c_uint64 * 4)(), C.c_uint64()
+        _check(load_library().pi_gguf_tensor_info(self.h, i, C.byref(name), C.byref(t), C.byref(nd), ne, C.byref(off)),
+               None)
+        return {"name": name.value.decode(), "type": t.value, "ne": list(ne)[: nd.value], "offset": off.value}
+
+    def find(self, name: str) -> int:
+        return load_library().pi_gguf_find_tensor(self.h, name.encode())
+
+    def tensor_data(self, i: int) -> np.ndarray:
+        p, n, err = C.c_void_p(), C.c_size_t(), C.create_string_buffer(256)
+        rc = load_library().pi_gguf_tensor_data(self.h, i, C.byref(p), C.byref(n), err, 256)
+        if rc != PI_OK:
+            raise PiError(rc, err.value.decode())
+        return np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p.value)) if n.value else np.empty(0, np.uint8)
+
+    # -- the model ---------------------------------------------------------------
+    def model_desc(self, max_layers: int = 512, max_eos: int = 64):
+        """(ModelDesc, keepalive) for pi_hip_model_bind: Config::from_gguf and
+        Model::load's tensor binding (model.rs:31-97, 487-601)."""
+        desc = ModelDesc()
+        layers = (LayerDesc * max_layers)()
+        eos = (C.c_uint32 * max_eos)()
+        err = C.create_string_buffer(512)
+        rc = load_library().pi_gguf_model_desc(self.h, C.byref(desc), layers, max_layers, eos, max_eos, err, 512)
+        if rc != PI_OK:
+            raise PiError(rc, err.value.decode())
+        return desc, (layers, eos)
+
+    def spec(self) -> "ModelSpec":
+        d, _ = self.model_desc()
+        return ModelSpec(n_layer=d.n_layer, n_embd=d.n_embd, n_ff=d.n_ff, n_head=d.n_head, n_head_kv=d.n_head_kv,
+                         head_dim=d.head_dim, n_vocab=d.n_vocab, n_rot=d.n_rot, rope_theta=d.rope_theta,
+                         rms_eps=d.rms_eps, eos_ids=tuple(d.eos_ids[i] for i in range(d.n_eos)))
+
+    def close(self) -> None:
+        if self.h:
+            load_library().pi_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        if sys.is_finalizing():
+            return
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 def _tdesc(entry) -> TensorDesc:
     t, ne0, ne1, buf = entry
     return TensorDesc(t, ne0, ne1, buf.ctypes.data)
@@ -580,19 +740,27 @@ def _tdesc(entry) -> TensorDesc:
 class HipEngine:
     """Device-resident Engine (model.rs:678-1352) on a HipBackend context."""
 
-    def __init__(self, backend: HipBackend, model: SynthModel, n_ctx: int):
-        self.b, self.model, self.n_ctx = backend, model, n_ctx
-        s = model.spec
-        T = model.tensors
-        self._layers = (LayerDesc * s.n_layer)()
-        names = {"attn_o": "attn_output"}
-        for l in range(s.n_layer):
-            for f in LAYER_TENSORS:
-                setattr(self._layers[l], f, _tdesc(T[f"blk.{l}.{names.get(f, f)}.weight"]))
-        self._eos = (C.c_uint32 * max(1, len(s.eos_ids)))(*s.eos_ids)
-        desc = ModelDesc(s.n_layer, s.n_embd, s.n_ff, s.n_head, s.n_head_kv, s.head_dim, s.n_rot, s.n_vocab,
-                         s.rope_theta, s.rms_eps, self._eos, len(s.eos_ids), _tdesc(T["token_embd.weight"]),
-                         _tdesc(T["output.weight"]), _tdesc(T["output_norm.weight"]), self._layers)
+    def __init__(self, backend: HipBackend, model, n_ctx: int):
+        """model: a SynthModel (host tensors) or a Gguf (tensors in the file's
+        mapping, bound as Engine::load binds them)."""
+        self.b, self.n_ctx = backend, n_ctx
+        if isinstance(model, Gguf):
+            desc, self._keep = model.model_desc()
+            self.model = SynthModel(model.spec())
+            self._gguf = model
+        else:
+            self.model = model
+            s = model.spec
+            T = model.tensors
+            self._layers = (LayerDesc * s.n_layer)()
+            names = {"attn_o": "attn_output"}
+            for l in range(s.n_layer):
+                for f in LAYER_TENSORS:
+                    setattr(self._layers[l], f, _tdesc(T[f"blk.{l}.{names.get(f, f)}.weight"]))
+            self._eos = (C.c_uint32 * max(1, len(s.eos_ids)))(*s.eos_ids)
+            desc = ModelDesc(s.n_layer, s.n_embd, s.n_ff, s.n_head, s.n_head_kv, s.head_dim, s.n_rot, s.n_vocab,
+                             s.rope_theta, s.rms_eps, self._eos, len(s.eos_ids), _tdesc(T["token_embd.weight"]),
+                             _tdesc(T["output.weight"]), _tdesc(T["output_norm.weight"]), self._layers)
         backend.bind_gen += 1
         self._gen = backend.bind_gen
         backend.check(backend.lib.pi_hip_model_bind(backend.ctx, C.byref(desc), n_ctx))
