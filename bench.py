@@ -59,9 +59,9 @@ MODEL_SEED, PROMPT_SEED, N_PROMPT, N_GEN = 1234, 77, 128, 256
 KV_BYTES_PER_POS = 2 * 40 * 36 * 64 * 4                                          # 737 280
 EMBD_ROW_BYTES = Q4K_K // 256 * 144                                               # 1 296
 # HBM bytes per k_mega launch from rocprofv3 FETCH_SIZE / WRITE_SIZE, each
-# scaled by what the counter reads for a 256 MiB copy; None until measured
-# (profiles/decode_minicpm2b_k_mega_traffic.md).
-K_MEGA_TRAFFIC_BYTES = None
+# scaled by what the counter reads for a 256 MiB copy, over one decode of
+# this workload (profiles/decode_minicpm2b_k_mega_traffic.md).
+K_MEGA_TRAFFIC_BYTES = round((1056837.97 * 1.99974 + 9539.16 * 1.0) * 1024)      # 2 173 887 ...
 # Same for the Q4_K GEMV launch (profiles/gemv_q4k_5760x2304_traffic.md).
 Q4K_TRAFFIC_BYTES = round((3714.5 * 1.9997 + 25.7 * 1.0) * 1024)
 
