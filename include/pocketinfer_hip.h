@@ -40,9 +40,18 @@ extern "C" {
 #define PI_TYPE_F32  0u
 #define PI_TYPE_F16  1u
 #define PI_TYPE_Q4_0 2u
+#define PI_TYPE_Q4_1 3u
+#define PI_TYPE_Q5_0 6u
+#define PI_TYPE_Q5_1 7u
 #define PI_TYPE_Q8_0 8u
+#define PI_TYPE_Q8_1 9u
+#define PI_TYPE_Q2_K 10u
+#define PI_TYPE_Q3_K 11u
 #define PI_TYPE_Q4_K 12u
+#define PI_TYPE_Q5_K 13u
 #define PI_TYPE_Q6_K 14u
+#define PI_TYPE_Q8_K 15u
+#define PI_TYPE_BF16 30u
 
 typedef struct pi_ctx pi_ctx;
 typedef struct pi_tensor pi_tensor;   /* weights resident in HBM */
@@ -62,7 +71,14 @@ void        pi_hip_destroy(pi_ctx *ctx);
 const char *pi_hip_name(const pi_ctx *ctx);
 /* util::Error message of the last failed call on ctx (util.rs:5-43). */
 const char *pi_last_error(const pi_ctx *ctx);
-/* OpenClBackend::supports (opencl.rs:432-434): 1 for Q4_K, Q6_K, Q4_0, Q8_0. */
+/* OpenClBackend::supports (opencl.rs:432-434): 1 for the int8-path types
+ * Q4_K, Q6_K, Q4_0, Q8_0 (quant_int.rs:75-80: Q8 of x, then the lanes
+ * epilogue), and for Q4_1, Q5_0, Q5_1, Q8_1, Q2_K, Q3_K, Q5_K, Q8_K and BF16,
+ * which the reference evaluates on its f32 path (quant::dot_row,
+ * quant.rs:361-441: products of dequantized weights and f32 x added in
+ * element order).  Q2_K, Q3_K and Q5_K follow the GGUF layout; the
+ * reference's decoders of those three index past their slices and panic
+ * (quant.rs:211, 254, 295-314). */
 int         pi_hip_supports(const pi_ctx *ctx, uint32_t ggml_type);
 /* OpenClBackend::selftest (opencl.rs:391-430): the same Q4_K and Q6_K vectors
  * and tolerance |gpu-cpu| <= 0.02|cpu| + 0.01, with cpu the f32 dot_row. */
@@ -91,11 +107,12 @@ int         pi_hip_matvec_noalloc(pi_ctx *ctx, const pi_tensor *w, const float *
 /* ---------------------------------------------------------------------------
  * Explicit upload and device-pointer GEMV (no counterpart call in the
  * reference; it replaces the implicit upload inside matvec, opencl.rs:439-460).
- * Weights are repacked on the device into a tiled layout: each row is cut
- * into units of whole blocks, one unit per lane of a 64-wide wavefront tile,
- * and the 16-byte chunks of the units are interleaved across the lanes so a
- * wavefront reads one contiguous span per load; f16 block scales of Q6_K,
- * Q4_0 and Q8_0 move to a plane of their own.  The native bytes are not kept.
+ * Weights of the int8-path types are repacked on the device into a tiled
+ * layout: each row is cut into units of whole blocks, one unit per lane of a
+ * 64-wide wavefront tile, and the 16-byte chunks of the units are interleaved
+ * across the lanes so a wavefront reads one contiguous span per load; f16
+ * block scales of Q6_K, Q4_0 and Q8_0 move to a plane of their own.  The
+ * native bytes are not kept.  The f32-path types keep their GGUF rows.
  * ------------------------------------------------------------------------- */
 int  pi_hip_upload(pi_ctx *ctx, uint32_t ggml_type, const void *host, size_t rows, size_t k,
                    pi_tensor **out);
@@ -103,12 +120,15 @@ void pi_hip_tensor_free(pi_ctx *ctx, pi_tensor *t);
 /* Bytes the tensor occupies in HBM (the algorithmic weight bytes). */
 size_t pi_hip_tensor_bytes(const pi_tensor *t);
 /* y[rows] = W x with x and y device pointers, on the context stream.
- * One launch: every workgroup quantizes x (k floats) to Q8 blocks in its LDS
- * (quant_int.rs:17-56), then runs the fused dequant + int8-dot GEMV
- * (quant_int.rs:330-419).  (Rows too long for LDS take a Q8 pre-pass into
- * context staging memory instead; same results.) */
+ * Int8-path types, one launch: every workgroup quantizes x (k floats) to Q8
+ * blocks in its LDS (quant_int.rs:17-56), then runs the fused dequant +
+ * int8-dot GEMV (quant_int.rs:330-419).  (Rows too long for LDS take a Q8
+ * pre-pass into context staging memory instead; same results.)  f32-path
+ * types: one lane per row adds its dequantized weights times x in element
+ * order (quant.rs:377-441). */
 int  pi_hip_gemv_dev(pi_ctx *ctx, const pi_tensor *w, const float *x_dev, float *y_dev);
-/* Same GEMV on already-quantized activations (device pointers, lane 0). */
+/* Same GEMV on already-quantized activations (device pointers, lane 0);
+ * int8-path types only (PI_E_UNSUPPORTED otherwise). */
 int  pi_hip_gemv_q8_dev(pi_ctx *ctx, const pi_tensor *w, const int8_t *q_dev, const float *d_dev,
                         const int32_t *sum_dev, float *y_dev);
 /* Times `iters` launches of the GEMV kernel alone on the context stream with

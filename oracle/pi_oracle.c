@@ -497,6 +497,12 @@ void po_dequant_row(uint32_t t, const uint8_t *data, size_t k, float *out) {
             break;
         }
         case PO_Q2_K: {
+            /* quant.rs:185-217 advances qp by 32 in every one of the four
+             * shifts, so its third shift indexes qs[64..] of a 64-byte slice
+             * and panics: the reference has no output for Q2_K.  This follows
+             * the GGUF format's layout instead (qs advances 32 bytes per 128
+             * elements, ggml's dequantize_row_q2_K) with the reference's float
+             * expressions. */
             float d = f16_at(p + 80), dmin = f16_at(p + 82);
             const uint8_t *scales = p, *qs = p + 16;
             size_t is = 0, n = 0, qp = 0;
@@ -509,13 +515,20 @@ void po_dequant_row(uint32_t t, const uint8_t *data, size_t k, float *out) {
                     sc = scales[is++];
                     dl = d * (float)(sc & 0xF); ml = dmin * (float)(sc >> 4);
                     for (int l = 0; l < 16; l++) out[done + n + 16 + l] = dl * (float)((qs[qp + 16 + l] >> shift) & 3) - ml;
-                    shift += 2; n += 32; qp += 32;
+                    shift += 2; n += 32;
                 }
+                qp += 32;
             }
             off += 84; done += 256;
             break;
         }
         case PO_Q3_K: {
+            /* quant.rs:218-259 indexes hm[qp + l] with qp advancing 32 per
+             * shift, past the 32-byte hmask slice from the second shift on,
+             * and panics.  This follows the GGUF format's layout (hmask
+             * indexed by l alone, bit m of it per shift; qs advancing 32 bytes
+             * per 128 elements, ggml's dequantize_row_q3_K) with the
+             * reference's float expressions. */
             float d_all = f16_at(p + 108);
             const uint8_t *qs = p + 32, *hm = p;
             uint32_t aux[4];
@@ -534,16 +547,17 @@ void po_dequant_row(uint32_t t, const uint8_t *data, size_t k, float *out) {
                 for (int r = 0; r < 4; r++) {
                     float dl = d_all * ((float)(int8_t)scales[is++] - 32.0f);
                     for (int l = 0; l < 16; l++) {
-                        int hi = (hm[qp + l] & m) ? 0 : 4;
+                        int hi = (hm[l] & m) ? 0 : 4;
                         out[done + n + l] = dl * (float)((int8_t)((qs[qp + l] >> shift) & 3) - hi);
                     }
                     dl = d_all * ((float)(int8_t)scales[is++] - 32.0f);
                     for (int l = 0; l < 16; l++) {
-                        int hi = (hm[qp + 16 + l] & m) ? 0 : 4;
+                        int hi = (hm[16 + l] & m) ? 0 : 4;
                         out[done + n + 16 + l] = dl * (float)((int8_t)((qs[qp + 16 + l] >> shift) & 3) - hi);
                     }
-                    shift += 2; m = (uint8_t)(m << 1); n += 32; qp += 32;
+                    shift += 2; m = (uint8_t)(m << 1); n += 32;
                 }
+                qp += 32;
             }
             off += 110; done += 256;
             break;
@@ -566,6 +580,12 @@ void po_dequant_row(uint32_t t, const uint8_t *data, size_t k, float *out) {
             break;
         }
         case PO_Q5_K: {
+            /* quant.rs:285-319 indexes qh[qp + l] with qp advancing 32 per
+             * 64 elements, past the 32-byte qh slice from the second pair of
+             * sub-blocks on, and panics.  This follows the GGUF format's
+             * layout (qh indexed by l alone, bits u1/u2 moving by two per
+             * pair, ggml's dequantize_row_q5_K) with the reference's float
+             * expressions. */
             float d = f16_at(p), dmin = f16_at(p + 2);
             const uint8_t *scales = p + 4, *qh = p + 16, *ql = p + 48;
             size_t is = 0, n = 0, qp = 0;
@@ -577,11 +597,11 @@ void po_dequant_row(uint32_t t, const uint8_t *data, size_t k, float *out) {
                 scale_min_k4(is + 1, scales, &sc, &m);
                 float d2 = d * (float)sc, m2 = dmin * (float)m;
                 for (int l = 0; l < 32; l++) {
-                    uint8_t q = (uint8_t)((ql[qp + l] & 0x0F) + ((qh[qp + l] & u1) ? 16 : 0));
+                    uint8_t q = (uint8_t)((ql[qp + l] & 0x0F) + ((qh[l] & u1) ? 16 : 0));
                     out[done + n + l] = d1 * (float)q - m1;
                 }
                 for (int l = 0; l < 32; l++) {
-                    uint8_t q = (uint8_t)((ql[qp + l] >> 4) + ((qh[qp + l] & u2) ? 16 : 0));
+                    uint8_t q = (uint8_t)((ql[qp + l] >> 4) + ((qh[l] & u2) ? 16 : 0));
                     out[done + n + 32 + l] = d2 * (float)q - m2;
                 }
                 qp += 32; n += 64; is += 2;

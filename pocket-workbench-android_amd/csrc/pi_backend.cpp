@@ -21,6 +21,7 @@
 #include "pi_kernels.h"
 #include "pi_mega.h"
 #include "pi_prefill.h"
+#include "pi_rowdot.h"
 #include "pi_sample.h"
 
 struct pi_tensor {
@@ -212,9 +213,32 @@ int grow_io(pi_ctx *c, size_t k, size_t rows) {
 // Upload native rows (host) and repack on the device.
 int upload_tensor(pi_ctx *c, uint32_t type, const void *host, size_t rows, size_t k, pi_tensor **out) {
     *out = nullptr;
-    if (!pi_gemv_type(type)) return fail(c, PI_E_UNSUPPORTED, "tensor type %u has no HIP kernel", type);
+    if (!pi_gemv_type(type) && !pi_row_type(type)) return fail(c, PI_E_UNSUPPORTED, "tensor type %u has no HIP kernel", type);
     if (!host || rows == 0 || rows > 0xFFFFFFFFu || k == 0 || k > 0xFFFFFFFFu)
         return fail(c, PI_E_INVALID, "invalid upload arguments");
+    if (pi_row_type(type)) {
+        // f32-path types keep their GGUF rows (BF16 rows of a multiple of 32)
+        const size_t rb = pi_row_bytes(type, k);
+        if (rb == 0 || k % 32 || pi_gemv_row_lds_bytes((uint32_t)k) > (size_t)c->max_lds)
+            return fail(c, PI_E_INVALID, "row length %zu not supported for type %u", k, type);
+        pi_tensor *t = new pi_tensor();
+        t->L = pi_layout{};
+        t->L.type = type;
+        t->L.k = (uint32_t)k;
+        t->L.rows = (uint32_t)rows;
+        t->L.bytes = (uint64_t)rb * rows;
+        int r = dalloc(c, &t->dev, t->L.bytes);
+        if (r) { delete t; return r; }
+        hipError_t e = hipMemcpyAsync(t->dev, host, t->L.bytes, hipMemcpyHostToDevice, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            dfree(t->dev);
+            delete t;
+            return fail(c, PI_E_HIP, "upload: %s", hipGetErrorString(e));
+        }
+        *out = t;
+        return PI_OK;
+    }
     pi_layout L;
     if (!pi_make_layout(type, (uint32_t)rows, (uint32_t)k, &L))
         return fail(c, PI_E_INVALID, "row length %zu not supported for type %u", k, type);
@@ -786,7 +810,7 @@ void pi_hip_destroy(pi_ctx *c) {
 const char *pi_hip_name(const pi_ctx *c) { return c ? c->name.c_str() : ""; }
 const char *pi_last_error(const pi_ctx *c) { return c ? c->err.c_str() : "no context"; }
 
-int pi_hip_supports(const pi_ctx *c, uint32_t t) { return c && pi_gemv_type(t) ? 1 : 0; }
+int pi_hip_supports(const pi_ctx *c, uint32_t t) { return c && (pi_gemv_type(t) || pi_row_type(t)) ? 1 : 0; }
 
 void pi_hip_clear_weight_cache(pi_ctx *c) {
     if (!c) return;
@@ -877,6 +901,7 @@ size_t pi_hip_tensor_bytes(const pi_tensor *t) { return t ? (size_t)t->L.bytes :
 
 int pi_hip_gemv_q8_dev(pi_ctx *c, const pi_tensor *w, const int8_t *q, const float *d, const int32_t *s, float *y) {
     if (!c || !w || !q || !d || !s || !y) return PI_E_INVALID;
+    if (!pi_gemv_type(w->L.type)) return fail(c, PI_E_UNSUPPORTED, "type %u has no int8 path", w->L.type);
     if (take_injected(c)) return PI_E_INJECTED;
     HIPC(c, launch_single_gemv(w, q, d, s, y, nullptr, PI_GEMV_OUT, c->stream));
     return PI_OK;
@@ -886,6 +911,10 @@ int pi_hip_gemv_q8_dev(pi_ctx *c, const pi_tensor *w, const int8_t *q, const flo
 // launch whose workgroups each quantize x into LDS; for rows too long for
 // that LDS, Q8 of x into the context's staging buffers, then the GEMV.
 static int enqueue_gemv_x(pi_ctx *c, const pi_tensor *w, const float *x, float *y) {
+    if (pi_row_type(w->L.type)) {
+        HIPC(c, pi_launch_gemv_row(w->L.type, w->dev, pi_row_bytes(w->L.type, w->L.k), w->L.rows, w->L.k, x, y, c->stream));
+        return PI_OK;
+    }
     if (pi_gemv_x_lds_bytes(w->L.type, w->L.g, w->L.k) <= (size_t)c->max_lds) {
         const pi_matset M = make_set({{w, y}});
         HIPC(c, pi_launch_gemv_x(M, x, gemv_blocks(w->L.ntiles), c->stream));
@@ -954,6 +983,8 @@ int pi_hip_copy_d2h(pi_ctx *c, void *dst, const void *src, size_t bytes) {
 int pi_hip_time_gemv(pi_ctx *c, const pi_tensor *const *ws, int n_copies, const int8_t *q, const float *d,
                      const int32_t *s, float *y, int iters, double *avg_us) {
     if (!c || !ws || n_copies < 1 || iters < 1 || !avg_us) return PI_E_INVALID;
+    for (int i = 0; i < n_copies; i++)
+        if (!ws[i] || !pi_gemv_type(ws[i]->L.type)) return fail(c, PI_E_UNSUPPORTED, "time_gemv: int8-path types only");
     hipEvent_t a, b;
     HIPC(c, hipEventCreate(&a));
     HIPC(c, hipEventCreate(&b));
@@ -999,7 +1030,7 @@ int pi_hip_matvec(pi_ctx *c, uint32_t type, const uint8_t *w, size_t w_bytes, si
                   size_t rows) {
     if (!c || !w || !x || !out || rows == 0 || k == 0) return c ? fail(c, PI_E_INVALID, "invalid matvec arguments") : PI_E_INVALID;
     if (take_injected(c)) return PI_E_INJECTED;
-    if (!pi_gemv_type(type)) return fail(c, PI_E_UNSUPPORTED, "type not supported");
+    if (!pi_gemv_type(type) && !pi_row_type(type)) return fail(c, PI_E_UNSUPPORTED, "type not supported");
     if (pi_row_bytes(type, k) * rows != w_bytes)
         return fail(c, PI_E_INVALID, "weight bytes %zu do not match %zu rows of k=%zu", w_bytes, rows, k);
     auto key = std::make_pair((uintptr_t)w, w_bytes);
@@ -1033,13 +1064,19 @@ int pi_hip_matvec_noalloc(pi_ctx *c, const pi_tensor *w, const float *x, float *
         const hipError_t e = (c->device >= 0 && c->device < kMaxDevices) ? g_scratch_err[c->device] : hipErrorInvalidDevice;
         return fail(c, PI_E_HIP, "matvec_noalloc: no staging address for device %d: %s", c->device, hipGetErrorString(e));
     }
-    if (pi_gemv_x_lds_bytes(w->L.type, w->L.g, w->L.k) > (size_t)c->max_lds)
+    const bool row = pi_row_type(w->L.type);
+    if (!row && pi_gemv_x_lds_bytes(w->L.type, w->L.g, w->L.k) > (size_t)c->max_lds)
         return fail(c, PI_E_UNSUPPORTED, "matvec_noalloc: row length %zu does not fit the kernel's LDS", k);
     float *xs = reinterpret_cast<float *>(c->scratch);
     float *ys = xs + PI_NOALLOC_MAX_K;
     HIPC(c, hipMemcpyAsync(xs, x, k * 4, hipMemcpyHostToDevice, c->stream));
-    const pi_matset M = make_set({{w, ys}});
-    HIPC(c, pi_launch_gemv_x(M, xs, gemv_blocks(w->L.ntiles), c->stream));
+    if (row) {
+        HIPC(c, pi_launch_gemv_row(w->L.type, w->dev, pi_row_bytes(w->L.type, k), (uint32_t)rows, (uint32_t)k, xs, ys,
+                                   c->stream));
+    } else {
+        const pi_matset M = make_set({{w, ys}});
+        HIPC(c, pi_launch_gemv_x(M, xs, gemv_blocks(w->L.ntiles), c->stream));
+    }
     HIPC(c, hipMemcpyAsync(out, ys, rows * 4, hipMemcpyDeviceToHost, c->stream));
     HIPC(c, hipStreamSynchronize(c->stream));
     return PI_OK;
@@ -1158,7 +1195,8 @@ int pi_hip_model_bind(pi_ctx *c, const pi_model_desc *m, uint32_t n_ctx) {
             !check_shape(L.ffn_down, m->n_ff, ne))
             return fail(c, PI_E_INVALID, "layer %u tensor shape mismatch", l);
     }
-    if (pi_type_block_elems(m->token_embd.type) == 0)
+    // token_embd rows are dequantized on the device (embed_elem)
+    if (m->token_embd.type != PI_TYPE_F32 && !pi_gemv_type(m->token_embd.type))
         return fail(c, PI_E_UNSUPPORTED, "token_embd type %u unsupported", m->token_embd.type);
     // kernel coverage: Q/K (and gate/up, and the head) are super-block types
     // with a fused norm prologue; V may differ from Q/K only between Q4_K and

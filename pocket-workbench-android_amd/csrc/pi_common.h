@@ -14,22 +14,33 @@
 #define PI_HD
 #endif
 
-// quant.rs:19-37 (the subset with HIP kernels, plus F32 for norm weights).
+// quant.rs:19-37: elements and bytes per block.
 inline size_t pi_type_block_elems(uint32_t t) {
     switch (t) {
-    case PI_TYPE_F32: return 1;
-    case PI_TYPE_Q4_0: case PI_TYPE_Q8_0: return 32;
-    case PI_TYPE_Q4_K: case PI_TYPE_Q6_K: return 256;
+    case PI_TYPE_F32: case PI_TYPE_F16: case PI_TYPE_BF16: return 1;
+    case PI_TYPE_Q4_0: case PI_TYPE_Q4_1: case PI_TYPE_Q5_0: case PI_TYPE_Q5_1: case PI_TYPE_Q8_0: case PI_TYPE_Q8_1:
+        return 32;
+    case PI_TYPE_Q2_K: case PI_TYPE_Q3_K: case PI_TYPE_Q4_K: case PI_TYPE_Q5_K: case PI_TYPE_Q6_K: case PI_TYPE_Q8_K:
+        return 256;
     default: return 0;
     }
 }
 inline size_t pi_type_block_bytes(uint32_t t) {
     switch (t) {
     case PI_TYPE_F32: return 4;
+    case PI_TYPE_F16: case PI_TYPE_BF16: return 2;
     case PI_TYPE_Q4_0: return 18;
+    case PI_TYPE_Q4_1: return 20;
+    case PI_TYPE_Q5_0: return 22;
+    case PI_TYPE_Q5_1: return 24;
     case PI_TYPE_Q8_0: return 34;
+    case PI_TYPE_Q8_1: return 36;
+    case PI_TYPE_Q2_K: return 84;
+    case PI_TYPE_Q3_K: return 110;
     case PI_TYPE_Q4_K: return 144;
+    case PI_TYPE_Q5_K: return 176;
     case PI_TYPE_Q6_K: return 210;
+    case PI_TYPE_Q8_K: return 292;
     default: return 0;
     }
 }
@@ -39,8 +50,19 @@ inline size_t pi_row_bytes(uint32_t t, size_t k) {
     if (be == 0 || k % be) return 0;
     return k / be * pi_type_block_bytes(t);
 }
+// Types with the int8 path (quant_int.rs:75-80): tiled layout, Q8 activations.
 inline bool pi_gemv_type(uint32_t t) {
     return t == PI_TYPE_Q4_K || t == PI_TYPE_Q6_K || t == PI_TYPE_Q4_0 || t == PI_TYPE_Q8_0;
+}
+// Types the reference evaluates on its f32 path (quant.rs:377-441) that have a
+// row kernel here (GGUF row layout; BF16 rows of a multiple of 32 elements).
+inline bool pi_row_type(uint32_t t) {
+    switch (t) {
+    case PI_TYPE_Q4_1: case PI_TYPE_Q5_0: case PI_TYPE_Q5_1: case PI_TYPE_Q8_1: case PI_TYPE_Q2_K: case PI_TYPE_Q3_K:
+    case PI_TYPE_Q5_K: case PI_TYPE_Q8_K: case PI_TYPE_BF16:
+        return true;
+    default: return false;
+    }
 }
 
 // util.rs:76-100: exact half -> single, subnormals included.

@@ -285,7 +285,7 @@ def _check(rc: int, ctx) -> None:
 # backend
 # ---------------------------------------------------------------------------
 class Tensor:
-    """Weights resident in HBM (tiled layout)."""
+    """Weights resident in HBM (tiled layout; GGUF rows for the f32-path types)."""
 
     def __init__(self, backend: "HipBackend", handle: int, t: int, rows: int, k: int):
         self._b, self.handle, self.type, self.rows, self.k = backend, handle, t, rows, k

@@ -24,9 +24,11 @@ def _rows(pih, t, rows, k, seed):
 def test_probe_name_supports_selftest(pih, backend):
     assert pih.probe() is not None and "gfx950" in pih.probe()
     assert "gfx950" in backend.name()
-    for t in (Q4_0, Q8_0, Q4_K, Q6_K):
+    for t in (Q4_0, Q8_0, Q4_K, Q6_K):               # int8 path
         assert backend.supports(t)
-    for t in (0, 1, 3, 6, 7, 10, 11, 13, 15, 30):
+    for t in (3, 6, 7, 9, 10, 11, 13, 15, 30):       # f32 path (tests/test_gpu_rowdot.py)
+        assert backend.supports(t)
+    for t in (0, 1, 4, 5, 16, 31):                   # F32 / F16 matrices, unknown ids
         assert not backend.supports(t)
     backend.selftest()
 
