@@ -22,7 +22,8 @@ Also measured here:
   gemv_q4k / gemv_q6k -- the standalone GEMVs of configs 1 and 2 with their
                 Q8 pass (the whole pi_hip_gemv_dev job) and without it,
                 rotating weight copies (twice the 256 MB Infinity Cache) so
-                the reads come from HBM;
+                the reads come from HBM; gemv_q5k_f32_path -- the same
+                5760 x 2304 shape in Q5_K on the reference's f32 path;
   prefill    -- the 2048-token prompt on the batched int8-MFMA prefill
                 kernels (64 chunks of 32), then the prompt extended by 512
                 tokens reusing the 2048 cached positions;
@@ -43,6 +44,8 @@ import os
 import sys
 import time
 from pathlib import Path
+
+import numpy as np
 
 REPO = Path(__file__).resolve().parent
 sys.path[:0] = [str(REPO), str(REPO / "pocket-workbench-android_amd")]
@@ -98,6 +101,30 @@ def time_gemv(b, t, rows, k, gen, copies, iters):
     for buf in (xd, yd, qd, dd, sd):
         buf.free()
     return whole, alone
+
+
+def q5k_rows(rows, k, seed=3):
+    """Random Q5_K blocks with finite f16 scales (GGUF row layout)."""
+    rng = np.random.default_rng(seed)
+    nb = rows * (k // 256)
+    blk = rng.integers(0, 256, size=(nb, 176), dtype=np.uint8)
+    for off in (0, 2):
+        blk[:, off:off + 2] = (rng.standard_normal(nb) * 0.02).astype(np.float16).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(-1).copy()
+
+
+def time_gemv_row(b, t, rows, k, w, copies, iters):
+    """us per launch of the f32-path GEMV (whole job: x f32 in HBM)."""
+    ws = [b.upload(t, w, rows, k) for _ in range(copies)]
+    x = pih.synth_normal(2, k)
+    xd, yd = b.to_device(x), b.alloc(rows * 4)
+    b.time_gemv_x(ws, xd.ptr, yd.ptr, max(copies, 8))                       # warm
+    us = b.time_gemv_x(ws, xd.ptr, yd.ptr, iters)
+    for wt in ws:
+        wt.free()
+    for buf in (xd, yd):
+        buf.free()
+    return us
 
 
 def gemv_entry(whole_us, alone_us, nbytes, kernel):
@@ -280,13 +307,24 @@ def run(args, skip, steps, warmup, b, t_start):
         return
 
     # -- standalone GEMVs of configs 1 and 2, HBM-cold ----------------------
-    g4 = g6 = None
+    g4 = g6 = g5 = None
     if not args.no_gemv:
         w4, a4 = time_gemv(b, pih.Q4_K, Q4K_ROWS, Q4K_K, pih.synth_q4k_random, 70, 700)
         w6, a6 = time_gemv(b, pih.Q6_K, Q6K_ROWS, Q6K_K, pih.synth_q6k_random, 3, 30)
-        g4 = gemv_entry(w4, a4, Q4K_LAUNCH_BYTES, "Q4_K GEMV 5760x2304: k_q8 + k_gemv<12,1,0>")
+        g4 = gemv_entry(w4, a4, Q4K_LAUNCH_BYTES,
+                        "Q4_K GEMV 5760x2304: k_gemv_x<12,1> (Q8 of x in its prologue); alone: k_gemv<12,1,0>")
         g4["traffic_gemv_alone"] = Q4K_TRAFFIC_BYTES
-        g6 = gemv_entry(w6, a6, Q6K_LAUNCH_BYTES, "Q6_K head GEMV 122753x2304: k_q8 + k_gemv<14,1,0>")
+        g6 = gemv_entry(w6, a6, Q6K_LAUNCH_BYTES,
+                        "Q6_K head GEMV 122753x2304: k_gemv_x<14,1> (Q8 of x in its prologue); alone: k_gemv<14,1,0>")
+        q5w = q5k_rows(Q4K_ROWS, Q4K_K)
+        u5 = time_gemv_row(b, pih.Q5_K, Q4K_ROWS, Q4K_K, q5w, 20, 100)
+        q5_bytes = q5w.nbytes + Q4K_K * 4 + Q4K_ROWS * 4
+        g5 = {"kernel": "Q5_K GEMV 5760x2304, the reference's f32 path (dot_row_scalar order): k_gemv_row<13>",
+              "bytes_per_launch": q5_bytes, "us": round(u5, 2),
+              "achieved_gbs": round(q5_bytes / (u5 * 1e-6) / 1e9, 1),
+              "frac": round(q5_bytes / (u5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+              "bound": "one dependent add per element per lane (latency), not HBM"}
+        log(f"gemv q5_k (f32 path): {g5}")
         log(f"gemv q4k: {g4}")
         log(f"gemv q6k: {g6}")
 
@@ -375,7 +413,7 @@ def run(args, skip, steps, warmup, b, t_start):
                      "us_per_launch": round(kern_us, 2), "launches_timed": kern_n,
                      "bytes_per_launch": round(launch_bytes), "weight_bytes": wbytes,
                      "kv_bytes_mean": round(kv_mean),
-                     "gemv_q4k": g4, "gemv_q6k": g6},
+                     "gemv_q4k": g4, "gemv_q6k": g6, "gemv_q5k_f32_path": g5},
         "decode_weight_roofline": {"weight_bytes_per_token": wbytes,
                                    "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / wbytes, 1),
                                    "frac": round(tps * wbytes / (HBM_PEAK_GBS * 1e9), 4)},

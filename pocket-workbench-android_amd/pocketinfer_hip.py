@@ -28,6 +28,7 @@ LIB_PATH = _HERE / "libpocketinfer_hip.so"
 
 # GGML type ids (quant.rs:3-17)
 F32, F16, Q4_0, Q8_0, Q4_K, Q6_K = 0, 1, 2, 8, 12, 14
+Q4_1, Q5_0, Q5_1, Q8_1, Q2_K, Q3_K, Q5_K, Q8_K, BF16 = 3, 6, 7, 9, 10, 11, 13, 15, 30   # f32-path types
 BLOCK = {F32: (1, 4), Q4_0: (32, 18), Q8_0: (32, 34), Q4_K: (256, 144), Q6_K: (256, 210)}
 
 PI_OK = 0
