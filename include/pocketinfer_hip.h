@@ -266,9 +266,10 @@ int  pi_hip_use_graphs(pi_ctx *ctx, int enable);
  * reference: the reference evaluates a token as a sequence of CPU loops. */
 int  pi_hip_use_persistent(pi_ctx *ctx, int enable);
 /* Prompt chunks of 2..32 tokens (and engine forwards of several consecutive
- * tokens) run on the batched int8-MFMA prefill kernels by default; enable =
- * 0 evaluates them one token at a time.  Results are identical either way
- * (the reference's multi-token float orders, model.rs:812-822, 1028-1038). */
+ * tokens) run on the batched int8-MFMA prefill kernels by default, in passes
+ * of up to 256 tokens that may span several chunks; enable = 0 evaluates them
+ * one token at a time.  Results are identical either way (the reference's
+ * multi-token float orders, model.rs:812-822, 1028-1038). */
 int  pi_hip_use_batch_prefill(pi_ctx *ctx, int enable);
 /* 1 when the bound model runs on the persistent kernel, 0 otherwise. */
 int  pi_hip_persistent_active(const pi_ctx *ctx);

@@ -133,7 +133,7 @@ struct pi_ctx {
     bool fail_next = false;
     bool use_graphs = true;   // replay captured graphs (else launch each kernel)
     bool use_persistent = true;  // one persistent kernel per token when the model fits
-    bool use_batch_prefill = true;  // chunks of 2..32 tokens on the MFMA prefill kernels
+    bool use_batch_prefill = true;  // multi-token chunks on the MFMA prefill kernels
     bool time_kernels = false;      // event pair around every decode forward of generate
     std::atomic<int> stop{0};
     std::map<std::pair<uintptr_t, size_t>, pi_tensor *> wcache;
@@ -628,8 +628,9 @@ bool use_pf(const pi_ctx *c, const Engine &e) { return c->use_batch_prefill && e
 
 pi_pf_mat pfmat(const pi_tensor *t) { return pi_pf_mat{t->dev, t->L}; }
 
-// One chunk of ntok (2..32) tokens at positions pos0.. through every layer
-// on the batched prefill kernels; the residual stream ends in pfX.
+// One pass of ntok (1..PI_PF_MAX_TOK) consecutive tokens at positions pos0..
+// through every layer on the batched prefill kernels; the residual stream
+// ends in pfX.
 hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, uint32_t pos0, uint32_t ntok) {
     hipStream_t s = c->stream;
     hipError_t r;
@@ -1309,7 +1310,7 @@ static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int 
     for (int i = 1; i < b; i++) consecutive &= pos[i] == pos[0] + i;
     if (b > 1 && consecutive && use_pf(c, *e)) {
         // a batch of more than one token: every token in the multi-token
-        // orders, in chunks of at most 32 on the batched prefill kernels
+        // orders, in passes of at most PI_PF_MAX_TOK on the batched kernels
         if (want_logits) {
             int r = set_state(c, *e, pos[b - 1], ids[b - 1], 0, 0);
             if (r) return r;
@@ -1509,15 +1510,17 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     // prompt token also computes logits and the first greedy id.
     const size_t last_chunk = (n - reused) % chunk == 0 ? chunk : (n - reused) % chunk;
     if (use_pf(c, *e)) {
-        // Reference chunks of 32 from `reused`: a chunk of more than one token
-        // runs on the batched prefill kernels; a chunk of one (only the last
-        // can be) in the batch-1 order.  The last chunk also computes the
-        // logits and the first greedy id of its last token.
+        // Reference chunks of 32 from `reused`: every token of a chunk of more
+        // than one token runs on the batched prefill kernels, in passes of up
+        // to PI_PF_MAX_TOK tokens that may span several chunks; a chunk of one
+        // (only the last can be) runs in the batch-1 order.  The last pass
+        // also computes the logits and the first greedy id of its last token.
+        const size_t batched_end = last_chunk == 1 ? n - 1 : n;
         while (off < n) {
             if (c->stop.load()) { stopped = true; break; }
-            const size_t end = std::min(n, off + chunk);
+            const size_t end = off < batched_end ? std::min(batched_end, off + PI_PF_MAX_TOK) : n;
             const bool last = end == n;
-            if (end - off == 1) {
+            if (off >= batched_end) {
                 if (mega) {
                     HIPC(c, mega_token(c, *e, (int32_t)off, prompt[off], nullptr, e->ids, true, true));
                 } else {

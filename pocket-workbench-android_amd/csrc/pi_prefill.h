@@ -1,6 +1,9 @@
-// Launchers of the batched prefill kernels (pi_prefill.hip): one chunk of up
-// to 32 prompt tokens evaluated together, in the float orders the reference
-// uses for a batch of more than one token (model.rs:812-822, 1028-1038).
+// Launchers of the batched prefill kernels (pi_prefill.hip): one pass of up
+// to PI_PF_MAX_TOK consecutive prompt tokens evaluated together, in the float
+// orders the reference uses for a batch of more than one token (model.rs:
+// 812-822, 1028-1038).  A token's values depend only on its own inputs and on
+// the KV rows of earlier positions, so a pass may span several of the
+// reference's 32-token chunks without changing any value.
 // All launch on `s` and return hipSuccess or the launch error.
 #pragma once
 
@@ -8,7 +11,7 @@
 
 #include "pi_common.h"
 
-constexpr uint32_t PI_PF_MAX_TOK = 32;
+constexpr uint32_t PI_PF_MAX_TOK = 256;
 
 // A weight matrix in the tiled layout (pi_common.h), as the prefill GEMM reads it.
 struct pi_pf_mat {
@@ -19,8 +22,8 @@ struct pi_pf_mat {
 // Token-major activations of a chunk: row t of a [ntok][n] matrix at t * n.
 // Q8 activations (the values of Q8Act, quant_int.rs:17-56) are laid out for
 // the MFMA operand loads: the 8 quants 8*ka..8*ka+7 of 32-element group G of
-// token t at byte ((G * 4 + ka) * 32 + t) * 8; d and the block sum of (G, t)
-// at index G * 32 + t.
+// token t at byte ((G * 4 + ka) * PI_PF_MAX_TOK + t) * 8; d and the block sum
+// of (G, t) at index G * PI_PF_MAX_TOK + t.
 struct pi_pf_q8 {
     int8_t *q;
     float *d;

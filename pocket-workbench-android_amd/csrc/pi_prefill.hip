@@ -1,4 +1,4 @@
-// Batched prefill for gfx950: a chunk of up to 32 prompt tokens per pass.
+// Batched prefill for gfx950: up to PI_PF_MAX_TOK consecutive prompt tokens per pass.
 //
 // The projections run on int8 MFMA: v_mfma_i32_16x16x32_i8 forms, for a tile
 // of 16 weight rows x 16 tokens, the exact int32 dot product of one
@@ -50,7 +50,7 @@ __device__ __forceinline__ v4i mfma16(long a, long b) {
 
 // ---------------------------------------------------------------------------
 // GEMM.  A workgroup of four wavefronts owns 16 rows of one matrix and 16
-// tokens of the chunk.  Every (row, token) output is 0 + t_0 + t_1 + ... in
+// tokens of the pass.  Every (row, token) output is 0 + t_0 + t_1 + ... in
 // the reference's term order (one term per 32-element group; Q6_K one per
 // 16-element group in (half, g, s) order).  The terms are formed in phases
 // of 16: in each phase wavefront w forms terms 4w..4w+3 for all 256
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
 }
 
 // ---------------------------------------------------------------------------
-// Embedding rows of the chunk.
+// Embedding rows of the pass.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_pf_embed(const uint8_t *__restrict__ E, uint32_t etype, uint64_t row_bytes,
                                                   const uint32_t *__restrict__ ids, uint32_t ne, float *__restrict__ X) {

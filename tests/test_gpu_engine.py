@@ -113,6 +113,21 @@ def test_tiny_generate_matches_oracle(pih, backend, oracle, tiny, n_prompt):
     assert _bits_equal(eng.logits(), ref.logits())
 
 
+@pytest.mark.parametrize("n_prompt", [300, 289, 257])
+def test_tiny_generate_passes_span_chunks(pih, backend, oracle, tiny, n_prompt):
+    """Prompts longer than one 256-token device pass: the passes group the
+    reference's 32-token chunks (300: passes of 256 + 44; 289: 256 + 32, then
+    the single-token last chunk; 257: 256, then the single token); ids and
+    final logits equal the oracle's."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=512)
+    ref = oracle.OracleEngine(tiny, n_ctx=512, threads=4)
+    prompt = [(i * 29 + 3) % 1000 for i in range(n_prompt)]
+    got, st = eng.generate(prompt, 8)
+    want, _ = ref.generate(prompt, 8)
+    assert got == want and st["prefill_tokens"] == n_prompt
+    assert _bits_equal(eng.logits(), ref.logits())
+
+
 def test_tiny_prefix_reuse(pih, backend, oracle, tiny):
     """tests/prefix_cache.rs:27-63 invariants on the device engine.  A context
     holds one engine, so the fresh run comes first."""
