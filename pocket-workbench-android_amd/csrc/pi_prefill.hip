@@ -49,28 +49,28 @@ __device__ __forceinline__ v4i mfma16(long a, long b) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMM.  A workgroup of four wavefronts owns 16 rows of one matrix and 16
-// tokens of the pass.  Every (row, token) output is 0 + t_0 + t_1 + ... in
-// the reference's term order (one term per 32-element group; Q6_K one per
-// 16-element group in (half, g, s) order).  The terms are formed in phases
-// of 16: in each phase wavefront w forms terms 4w..4w+3 for all 256
-// (row, token) pairs - one int8 MFMA (lane l: A row r0 + l%16 with group
-// elements 8*(l/16)..+7; B token l%16; D rows 4*(l/16)+i) and the float
-// term per pair - into an LDS plane; after a barrier, thread p adds the
-// phase's terms of pair p in order.  The weight chunks a phase needs are
-// staged into LDS by the whole workgroup (whole 16-byte chunks, one phase
-// ahead), the activation operands come in token-contiguous runs, and the
-// per-row constants of the terms (f16 scales, 6-bit sub-block scales/mins,
-// Q6_K d*scale) are decoded once into LDS.  Two planes and two weight
-// buffers alternate: one barrier per phase.
+// GEMM.  A workgroup of four wavefronts owns 16 rows of one matrix and 64
+// tokens of the pass; wavefront w serves tokens 16w..16w+15 of them.  Every
+// (row, token) output is 0 + t_0 + t_1 + ... in the reference's term order
+// (one term per 32-element group; Q6_K one per 16-element group in
+// (half, g, s) order).  Each term is one int8 MFMA (lane l: A row
+// r0 + l%16 with group elements 8*(l/16)..+7; B token l%16; D rows
+// 4*(l/16)+i) and the float term per pair, added at once to the pair's sum
+// in a register: a lane keeps the sums of rows 4*(l/16)..+3 for its token.
+// The weight chunks of a phase of 16 terms are staged into LDS by the whole
+// workgroup (whole 16-byte chunks, one phase ahead, two buffers: one barrier
+// per phase) and read by all four wavefronts; the activation operands of the
+// next kPfActDepth terms are in flight in registers; the per-row constants
+// of the terms (f16 scales, 6-bit sub-block scales/mins, Q6_K d*scale) are
+// decoded once into LDS.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kPfRows = 16;
 constexpr uint32_t kPfThreads = 256;
 constexpr uint32_t kPfPhase = 16;                   // terms per row per phase
-constexpr uint32_t kPfTermsPerWave = kPfPhase / 4;
-constexpr uint32_t kPfTokPad = 20;                  // floats per row of a term plane (16 tokens + 4)
-constexpr uint32_t kPfPlane = kPfRows * kPfTokPad;  // floats per term plane: [row][token]
+constexpr uint32_t kPfTokWg = 64;                   // tokens per workgroup
+constexpr uint32_t kPfActDepth = 8;                 // terms whose activation operands are in flight
 constexpr uint32_t kPfMaxSeg = 3;
+static_assert(kPfPhase % kPfActDepth == 0, "the operand ring index is static within a phase");
 
 // Row r of a tiled matrix: its tile, the tile's lane count and the lane of
 // the row's first unit.
@@ -252,8 +252,8 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
     const WV W = seg == 0 ? S.W[0] : (seg == 1 ? S.W[1] : S.W[2]);
     float *const out = seg == 0 ? S.out[0] : (seg == 1 ? S.out[1] : S.out[2]);
     const uint32_t wg0 = seg == 0 ? 0u : (seg == 1 ? S.wg_end[0] : S.wg_end[1]);
-    const uint32_t nth = (ntok + 15) / 16;
-    const uint32_t rg = (wg - wg0) / nth, th = (wg - wg0) - rg * nth;
+    const uint32_t ntb = (ntok + kPfTokWg - 1) / kPfTokWg;
+    const uint32_t rg = (wg - wg0) / ntb, tb = (wg - wg0) - rg * ntb;
     const uint32_t r0 = rg * kPfRows;
     const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
     const uint32_t ka = lane >> 4, li = lane & 15u;
@@ -262,9 +262,7 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
     const uint32_t tpr = T == PI_TYPE_Q6_K ? 16 * nb : (T == PI_TYPE_Q4_K ? 8 * nb : nb);   // terms per row
     const uint32_t nph = (tpr + kPfPhase - 1) / kPfPhase;
     float *cst = lds;
-    float *pl0 = lds + (((uint64_t)nb * PfLds<T>::floats_per_block + 3) & ~3ull);
-    float *pl1 = pl0 + kPfPhase * kPfPlane;
-    uint4 *wb0 = reinterpret_cast<uint4 *>(pl1 + kPfPhase * kPfPlane);
+    uint4 *wb0 = reinterpret_cast<uint4 *>(lds + (((uint64_t)nb * PfLds<T>::floats_per_block + 3) & ~3ull));
     uint4 *wb1 = wb0 + kPfRows * ST::WS;
 
     // ---- staging: this thread's pieces -----------------------------------
@@ -312,24 +310,20 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
     };
 
     // ---- activation operands -----------------------------------------------
-    const uint32_t n = th * 16 + li;   // this lane's MFMA token
+    // this lane's MFMA token; lanes past the pass read the last token's operands
+    const uint32_t n = tb * kPfTokWg + w * 16 + li, nc = min(n, ntok - 1);
     auto act_group = [&](uint32_t tg) -> uint32_t {
         if constexpr (T == PI_TYPE_Q6_K) return (tg >> 4) * 8 + 4 * ((tg >> 3) & 1u) + (tg & 3u);
         else return tg;
     };
-    struct PhaseAct {
-        TermAct A[kPfTermsPerWave];
-    };
-    auto load_act = [&](uint32_t ph) {
-        PhaseAct P;
-#pragma unroll
-        for (uint32_t j = 0; j < kPfTermsPerWave; j++) {
-            const uint32_t a = act_group(min(ph * kPfPhase + w * kPfTermsPerWave + j, tpr - 1));
-            P.A[j].b = *gld(reinterpret_cast<const uint2 *>(aq + pfq_off(a, ka, n)));
-            P.A[j].da = *gld(ad + a * PI_PF_MAX_TOK + n);
-            if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q4_0) P.A[j].as = *gld(as + a * PI_PF_MAX_TOK + n);
-        }
-        return P;
+    auto load_act = [&](uint32_t tg) {
+        const uint32_t a = act_group(min(tg, tpr - 1));
+        TermAct X;
+        X.b = *gld(reinterpret_cast<const uint2 *>(aq + pfq_off(a, ka, nc)));
+        X.da = *gld(ad + a * PI_PF_MAX_TOK + nc);
+        X.as = 0;
+        if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q4_0) X.as = *gld(as + a * PI_PF_MAX_TOK + nc);
+        return X;
     };
 
     // the 4 terms of rows 4*ka..4*ka+3 for this lane's token
@@ -394,52 +388,47 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
     };
 
     // ---- phases ---------------------------------------------------------------
-    float acc = 0.0f;
-    // pair of this thread: token pn, row pr.  Plane address row * 20 + token:
-    // the 64 lanes of a wavefront (4 tokens x 16 rows) and of each term
-    // write (16 tokens x rows 4*ka + i) fall on 64 distinct banks.
-    const uint32_t pn = tid >> 4, pr = tid & 15u;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    TermAct R[kPfActDepth];
     Staged SW = load_pieces(0);
-    PhaseAct TA = load_act(0);
+#pragma unroll
+    for (uint32_t j = 0; j < kPfActDepth; j++) R[j] = load_act(j);
     decode_consts<T>(W, r0, nb, cst);
     store_pieces(SW, wb0);
     SW = load_pieces(min(1u, nph - 1));
     __syncthreads();
+    auto step = [&](const uint4 *wb, uint32_t ph, uint32_t tg, TermAct &X) {
+        float t[4];
+        term4(X, wb, ph, tg, t);
+        X = load_act(tg + kPfActDepth);
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = acc[i] + t[i];
+    };
     for (uint32_t ph = 0; ph < nph; ph++) {
-        const PhaseAct TN = load_act(min(ph + 1, nph - 1));
         const uint4 *wb = (ph & 1u) ? wb1 : wb0;
-        float *pl = (ph & 1u) ? pl1 : pl0;
+        const uint32_t tg0 = ph * kPfPhase;
+        if (tg0 + kPfPhase <= tpr) {
 #pragma unroll
-        for (uint32_t j = 0; j < kPfTermsPerWave; j++) {
-            const uint32_t jj = w * kPfTermsPerWave + j, tg = ph * kPfPhase + jj;
-            if (tg < tpr) {
-                float t[4];
-                term4(TA.A[j], wb, ph, tg, t);
+            for (uint32_t j = 0; j < kPfPhase; j++) step(wb, ph, tg0 + j, R[j % kPfActDepth]);
+        } else {
 #pragma unroll
-                for (int i = 0; i < 4; i++) pl[jj * kPfPlane + (4 * ka + i) * kPfTokPad + li] = t[i];
-            }
+            for (uint32_t j = 0; j < kPfPhase; j++)
+                if (tg0 + j < tpr) step(wb, ph, tg0 + j, R[j % kPfActDepth]);
         }
         if (ph + 1 < nph) store_pieces(SW, (ph & 1u) ? wb0 : wb1);
         SW = load_pieces(min(ph + 2, nph - 1));
         __syncthreads();
-        const float *col = pl + pr * kPfTokPad + pn;
-        const uint32_t lim = min(kPfPhase, tpr - ph * kPfPhase);
-        if (lim == kPfPhase) {
-            float v[kPfPhase];
-#pragma unroll
-            for (uint32_t q = 0; q < kPfPhase; q++) v[q] = col[q * kPfPlane];
-#pragma unroll
-            for (uint32_t q = 0; q < kPfPhase; q++) acc += v[q];
-        } else {
-            for (uint32_t q = 0; q < lim; q++) acc += col[q * kPfPlane];
-        }
-        TA = TN;
     }
-    const uint32_t tok = th * 16 + pn, r = r0 + pr;
-    if (tok < ntok && r < W.rows) {
-        float *o = out + (uint64_t)tok * W.rows + r;
-        const float v = 0.0f + acc;
-        *o = resid ? *o + v : v;
+    if (n < ntok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t r = r0 + 4 * ka + i;
+            if (r < W.rows) {
+                float *o = out + (uint64_t)n * W.rows + r;
+                const float v = 0.0f + acc[i];
+                *o = resid ? *o + v : v;
+            }
+        }
     }
 }
 
@@ -832,7 +821,7 @@ hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg
         if (M[i].L.type != t || M[i].L.k != k || M[i].L.rows == 0) return hipErrorInvalidValue;
         S.W[i] = to_wv(M[i]);
         S.out[i] = out[i];
-        wgs += (M[i].L.rows + kPfRows - 1) / kPfRows * ((ntok + 15) / 16);
+        wgs += (M[i].L.rows + kPfRows - 1) / kPfRows * ((ntok + kPfTokWg - 1) / kPfTokWg);
         S.wg_end[i] = wgs;
     }
     S.nseg = nseg;
@@ -855,8 +844,8 @@ hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg
     case PI_TYPE_Q8_0: ws = PfStage<PI_TYPE_Q8_0>::WS; break;
     default: ws = PfStage<PI_TYPE_Q4_0>::WS; break;
     }
-    const size_t lds = (((cfl + 3) & ~(size_t)3) + 2 * (size_t)kPfPhase * kPfPlane) * 4 + 2 * (size_t)kPfRows * ws * 16;
-    if (lds > 80 * 1024 || nb > 65535) return hipErrorInvalidValue;   // two workgroups per CU
+    const size_t lds = ((cfl + 3) & ~(size_t)3) * 4 + 2 * (size_t)kPfRows * ws * 16;
+    if (lds > 64 * 1024 || nb > 65535) return hipErrorInvalidValue;
     const dim3 grid(wgs), block(kPfThreads);
     auto launch = [&](auto kern) {
         hipError_t e = hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
