@@ -118,6 +118,7 @@ struct Engine {
     // batched prefill (pi_prefill.hip): token-major chunk buffers
     bool pf_ok = false;
     float *pfX = nullptr, *pfQ = nullptr, *pfK = nullptr, *pfV = nullptr, *pfG = nullptr, *pfU = nullptr;
+    float *pfS = nullptr;   // attention scores of a pass: [token][head][n_ctx]
     int8_t *pfq = nullptr;
     float *pfd = nullptr;
     int32_t *pfs = nullptr;
@@ -329,7 +330,7 @@ void engine_free(Engine *e) {
                     (void *)e->mega_abort, (void *)e->mega_trace, (void *)e->mega_amax, (void *)e->mega_aexp})
         dfree(p);
     for (void *p : {(void *)e->pfX, (void *)e->pfQ, (void *)e->pfK, (void *)e->pfV, (void *)e->pfG, (void *)e->pfU,
-                    (void *)e->pfq, (void *)e->pfd, (void *)e->pfs, (void *)e->pf_ids})
+                    (void *)e->pfS, (void *)e->pfq, (void *)e->pfd, (void *)e->pfs, (void *)e->pf_ids})
         dfree(p);
     for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
                     (void *)e->sin_tab, (void *)e->x, (void *)e->q, (void *)e->k, (void *)e->v, (void *)e->h,
@@ -609,16 +610,13 @@ int build_prefill(pi_ctx *c, Engine &e) {
     e.pf_ok = false;
     const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
     if (e.dh != 64 || e.n_embd / 32 > 256 || e.n_rot / 2 > 32) return PI_OK;
-    int maxlds = 0;
-    if (hipDeviceGetAttribute(&maxlds, hipDeviceAttributeSharedMemPerBlockOptin, c->device) != hipSuccess) maxlds = 65536;
-    if (pi_pf_attn_lds_bytes(e.n_ctx) > (size_t)maxlds) return PI_OK;
     const uint64_t T = PI_PF_MAX_TOK;
     const uint64_t kmax = std::max(std::max(e.n_embd, e.n_ff), qdim);
     int r;
     if ((r = dalloc(c, &e.pfX, T * e.n_embd)) || (r = dalloc(c, &e.pfQ, T * qdim)) || (r = dalloc(c, &e.pfK, T * kdim)) ||
         (r = dalloc(c, &e.pfV, T * kdim)) || (r = dalloc(c, &e.pfG, T * e.n_ff)) || (r = dalloc(c, &e.pfU, T * e.n_ff)) ||
         (r = dalloc(c, &e.pfq, T * kmax)) || (r = dalloc(c, &e.pfd, T * kmax / 32)) || (r = dalloc(c, &e.pfs, T * kmax / 32)) ||
-        (r = dalloc(c, &e.pf_ids, 2 * T)))
+        (r = dalloc(c, &e.pfS, T * e.n_head * pi_pf_score_stride(e.n_ctx))) || (r = dalloc(c, &e.pf_ids, 2 * T)))
         return r;
     e.pf_ok = true;
     return PI_OK;
@@ -656,7 +654,7 @@ hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, u
         }
         K(pi_pf_rope_kv(e.pfQ, e.pfK, e.pfV, e.cos_tab, e.sin_tab, pos0, ntok, e.n_head, e.n_kv, e.n_rot / 2, kc, vc,
                         e.n_ctx, s));
-        K(pi_pf_attn(e.pfQ, kc, vc, pos0, ntok, e.n_head, e.n_kv, e.n_ctx, scale, A, s));
+        K(pi_pf_attn(e.pfQ, kc, vc, pos0, ntok, e.n_head, e.n_kv, e.n_ctx, scale, e.pfS, A, s));
         K(pi_pf_gemm(pfmat(L.o), A, ntok, e.pfX, true, s));
         K(pi_pf_norm_q8(e.pfX, L.ffn_norm, e.n_embd, e.eps, ntok, A, s));
         {

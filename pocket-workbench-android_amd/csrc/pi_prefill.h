@@ -50,9 +50,10 @@ hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *
                          uint32_t pos0, uint32_t ntok, uint32_t n_head, uint32_t n_kv, uint32_t half, float *kc,
                          float *vc, uint32_t n_ctx, hipStream_t s);
 // Attention of every token over positions 0..its own (model.rs:993-1087,
-// multi-token orders), then Q8 of the output.
+// multi-token orders), then Q8 of the output.  scores: scratch of
+// PI_PF_MAX_TOK * n_head * pi_pf_score_stride(n_ctx) floats.
+constexpr uint64_t pi_pf_score_stride(uint32_t n_ctx) { return ((uint64_t)n_ctx + 31) & ~31ull; }
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
-                      uint32_t n_kv, uint32_t n_ctx, float scale, pi_pf_q8 out, hipStream_t s);
-size_t pi_pf_attn_lds_bytes(uint32_t n_ctx);
+                      uint32_t n_kv, uint32_t n_ctx, float scale, float *scores, pi_pf_q8 out, hipStream_t s);
 // h = silu(gate) * up (model.rs:1111-1115), then Q8 of h.
 hipError_t pi_pf_swiglu_q8(const float *G, const float *U, uint32_t ntok, uint32_t n_ff, pi_pf_q8 out, hipStream_t s);

@@ -573,12 +573,17 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(float *__restrict__ Q, const
 // then V, rows are staged through two LDS buffers 64 positions per step by
 // wavefronts 0-3, each step's rows loaded into registers two steps ahead
 // (one barrier per step).
-// Scores (model.rs:1028-1038, scalar dot in d order, * scale): wavefront t
-// serves token t, lane = position.  Then e_p = exp(s_p - max) lane-parallel,
-// and a flag per step if any e_p is 0.  Values (f32_axpy order, products
-// rounded, e_p == 0 skipped): wavefront t adds e_p * v_p[d] in position
-// order, lane = dimension, from the transposed V step; meanwhile lane t of
-// wavefront 4 adds sum += e_p of token t in position order.
+// Pass 1, scores (model.rs:1028-1038, scalar dot in d order, * scale):
+// wavefront t serves token t, lane = position; each score goes to the
+// token's row of a score scratch in global memory, and the maximum is kept.
+// Pass 2, per step: wavefront t reads its 64 scores back (loaded two steps
+// ahead), forms e_p = exp(s_p - max) lane-parallel into an LDS step buffer,
+// then adds e_p * v_p[d] in position order (f32_axpy order, model.rs:
+// 1056-1074: products rounded, e_p == 0 skipped), lane = dimension, from the
+// transposed V step; lane t of wavefront 4 adds sum += e_p of token t in
+// position order, one step behind.  V is staged as blocks of 4 positions x
+// 4 dimensions per thread, transposed in registers, so its LDS writes are
+// 16 bytes wide and free of bank conflicts.
 // Output acc * (1/sum), then Q8 of the head's 64 values.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kAttStep = 64;               // positions per staged step
@@ -587,18 +592,19 @@ constexpr uint32_t kKRow = 68;                  // floats per staged K row
 constexpr uint32_t kVRow = kAttStep + 4;        // floats per staged transposed V row
 constexpr uint32_t kAttBuf = kAttStep * kKRow;  // floats per staging buffer (>= 64 * kVRow)
 static_assert(kAttBuf >= 64 * kVRow, "staging buffer holds a transposed V step");
+constexpr uint32_t kAttLdsFloats = 2 * kAttBuf + 4 * 64 + 2 * 4 * kAttStep + 16;
 
 __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
                                                          const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
                                                          uint32_t n_head, uint32_t group, uint32_t n_ctx, float scale,
-                                                         int8_t *__restrict__ oq, float *__restrict__ od,
-                                                         int32_t *__restrict__ os) {
+                                                         float *__restrict__ scr, int8_t *__restrict__ oq,
+                                                         float *__restrict__ od, int32_t *__restrict__ os) {
     constexpr uint32_t DH = 64;
-    extern __shared__ __align__(16) float lds[];
+    __shared__ __align__(16) float lds[kAttLdsFloats];
     float *const buf0 = lds, *const buf1 = lds + kAttBuf;
     float *qs = lds + 2 * kAttBuf;              // 4 x 64
-    float *misc = qs + 4 * DH;                  // 16 floats: per-token max and sum
-    uint32_t *zflag = reinterpret_cast<uint32_t *>(misc + 16);   // [4][nsteps]
+    float *eb = qs + 4 * DH;                    // [2][4][64]: e of a step per token, two steps alternating
+    float *misc = eb + 2 * 4 * kAttStep;        // per-token sums
     // Workgroup b runs on XCD b % 8 (round-robin dispatch): every workgroup of
     // head h gets b % 8 == h % 8, so a head's K/V rows are read into one L2.
     const uint32_t ntg = (ntok + 3) / 4, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
@@ -612,73 +618,85 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
     const uint32_t pos_t = pos0 + t;
     const uint32_t n_all = pos0 + min(4 * tg + 3, ntok - 1) + 1;
     const uint32_t nsteps = (n_all + kAttStep - 1) / kAttStep;
-    const uint32_t scs = (n_ctx + 3) & ~3u;    // row stride of the scores
-    float *sc = reinterpret_cast<float *>(zflag + 4 * ((nsteps + 3) & ~3u));   // [4][scs] scores, then e
-    float *sct = sc + (uint64_t)tok * scs;
     const uint32_t kvh = h / group, qdim = n_head * DH;
     const float *kbase = kc + (uint64_t)kvh * n_ctx * DH, *vbase = vc + (uint64_t)kvh * n_ctx * DH;
+    // this token's scores; rows are whole 128-byte lines apart, so no other
+    // wavefront touches a line of this row
+    float *const srow = scr + ((uint64_t)min(t, ntok - 1) * n_head + h) * pi_pf_score_stride(n_ctx);
 
     if (w < 4) qs[tok * DH + lane] = t < ntok ? Q[(uint64_t)t * qdim + h * DH + lane] : 0.0f;
-    for (uint32_t i = tid; i < 4 * nsteps; i += kAttThreads) zflag[i] = 0u;
 
-    // staging (wavefronts 0-3): row i = tid / 4 of the step, float4 columns 4*(tid%4)..+3
-    const uint32_t srow = tid >> 2, sf = (tid & 3u) * 4u;
     struct Rows {
         float4 v[4];
     };
-    // rows of wavefronts 4+ are a clamped in-bounds copy of row 0 (never stored)
-    auto load_rows = [&](const float *base, uint32_t c) -> Rows {
-        const uint32_t p = stager ? min(c * kAttStep + srow, n_all - 1) : 0u;
-        const float4 *src = reinterpret_cast<const float4 *>(base + (uint64_t)p * DH) + (stager ? sf : 0u);
+    // K (wavefronts 0-3): row tid / 4 of the step, float4 columns 4*(tid%4)..+3.
+    // V: positions 4*(tid%16)..+3, float4 column tid/16.  Rows of wavefront 4
+    // are a clamped in-bounds copy of row 0 (never stored).
+    auto load_k = [&](uint32_t c) -> Rows {
+        const uint32_t p = stager ? min(c * kAttStep + (tid >> 2), n_all - 1) : 0u;
+        const float4 *src = reinterpret_cast<const float4 *>(kbase + (uint64_t)p * DH) + (stager ? (tid & 3u) * 4u : 0u);
         Rows R;
 #pragma unroll
         for (int j = 0; j < 4; j++) R.v[j] = src[j];
         return R;
     };
+    auto load_v = [&](uint32_t c) -> Rows {
+        const uint32_t rb = tid & 15u, cb = stager ? tid >> 4 : 0u;
+        Rows R;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t p = stager ? min(c * kAttStep + 4 * rb + j, n_all - 1) : 0u;
+            R.v[j] = reinterpret_cast<const float4 *>(vbase + (uint64_t)p * DH)[cb];
+        }
+        return R;
+    };
     auto store_k = [&](const Rows R, float *bf) {
         if (!stager) return;
+        const uint32_t srw = tid >> 2, sf = (tid & 3u) * 4u;
 #pragma unroll
-        for (int j = 0; j < 4; j++) reinterpret_cast<float4 *>(bf + srow * kKRow)[sf + j] = R.v[j];
+        for (int j = 0; j < 4; j++) reinterpret_cast<float4 *>(bf + srw * kKRow)[sf + j] = R.v[j];
     };
     auto store_vt = [&](const Rows R, float *bf) {
         if (!stager) return;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t d = 4 * (sf + j);
-            bf[(d + 0) * kVRow + srow] = R.v[j].x;
-            bf[(d + 1) * kVRow + srow] = R.v[j].y;
-            bf[(d + 2) * kVRow + srow] = R.v[j].z;
-            bf[(d + 3) * kVRow + srow] = R.v[j].w;
-        }
+        const uint32_t rb = tid & 15u, cb = tid >> 4;
+        float *d0 = bf + (4 * cb) * kVRow + 4 * rb;
+        *reinterpret_cast<float4 *>(d0) = make_float4(R.v[0].x, R.v[1].x, R.v[2].x, R.v[3].x);
+        *reinterpret_cast<float4 *>(d0 + kVRow) = make_float4(R.v[0].y, R.v[1].y, R.v[2].y, R.v[3].y);
+        *reinterpret_cast<float4 *>(d0 + 2 * kVRow) = make_float4(R.v[0].z, R.v[1].z, R.v[2].z, R.v[3].z);
+        *reinterpret_cast<float4 *>(d0 + 3 * kVRow) = make_float4(R.v[0].w, R.v[1].w, R.v[2].w, R.v[3].w);
     };
-    // Runs body(c, buffer of step c) for every step; rows of step c + 1 are
-    // stored while step c is used, rows of step c + 2 are in flight.
-    auto stream = [&](const float *base, auto transposed, auto &&body) {
+    // Runs body(c, buffer of step c, parity of c) for every step; rows of step
+    // c + 1 are stored while step c is used, rows of step c + 2 are in flight.
+    auto stream = [&](auto transposed, auto &&body) {
+        auto load = [&](uint32_t c) {
+            if constexpr (decltype(transposed)::value) return load_v(c);
+            else return load_k(c);
+        };
         auto put = [&](const Rows R, float *bf) {
             if constexpr (decltype(transposed)::value) store_vt(R, bf);
             else store_k(R, bf);
         };
-        Rows A = load_rows(base, 0);
-        Rows B = load_rows(base, min(1u, nsteps - 1));
+        Rows A = load(0);
+        Rows B = load(min(1u, nsteps - 1));
         put(A, buf0);
         __syncthreads();
-        A = load_rows(base, min(2u, nsteps - 1));
+        A = load(min(2u, nsteps - 1));
         for (uint32_t c = 0; c < nsteps; c += 2) {
-            body(c, buf0);
+            body(c, buf0, std::integral_constant<uint32_t, 0>{});
             if (c + 1 < nsteps) put(B, buf1);
             __syncthreads();
             if (c + 1 >= nsteps) break;
-            B = load_rows(base, min(c + 3, nsteps - 1));
-            body(c + 1, buf1);
+            B = load(min(c + 3, nsteps - 1));
+            body(c + 1, buf1, std::integral_constant<uint32_t, 1>{});
             if (c + 2 < nsteps) put(A, buf0);
             __syncthreads();
-            A = load_rows(base, min(c + 4, nsteps - 1));
+            A = load(min(c + 4, nsteps - 1));
         }
     };
 
     // ---- pass 1: scores and maximum -------------------------------------
     float mx = -INFINITY;
-    stream(kbase, std::false_type{}, [&](uint32_t c, const float *cur) {
+    stream(std::false_type{}, [&](uint32_t c, const float *cur, auto) {
         const uint32_t p = c * kAttStep + lane;
         if (valid && p <= pos_t) {
             const float4 *kr = reinterpret_cast<const float4 *>(cur + lane * kKRow);
@@ -693,37 +711,54 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                 s += qq.w * kk.w;
             }
             s = s * scale;
-            sct[p] = s;
+            srow[p] = s;
             mx = fmaxf(mx, s);
         }
     });
 #pragma unroll
     for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
 
-    // ---- e_p = exp(s_p - max), zero flags per step -------------------------
-    if (valid) {
-        for (uint32_t c = 0; c < nsteps; c++) {
-            const uint32_t p = c * kAttStep + lane;
-            bool zero = false;
-            if (p <= pos_t) {
-                const float e = pi_expf(sct[p] - mx);
-                sct[p] = e;
-                zero = e == 0.0f;
-            }
-            if (__ballot(zero) && lane == 0) zflag[tok * nsteps + c] = 1u;
-        }
-    }
-    __syncthreads();
-
-    // ---- pass 2: sums in position order ------------------------------------
+    // ---- pass 2: e, then the sums in position order --------------------------
     float acc = 0.0f, sum = 0.0f;
     const uint32_t stok = lane & 3u, st_t = 4 * tg + stok;   // wavefront 4: lane = token
-    stream(vbase, std::true_type{}, [&](uint32_t c, const float *cur) {
+    // scores of steps 0 and 1 (this lane's position, clamped to written ones)
+    float sA = 0.0f, sB = 0.0f;
+    if (valid) {
+        sA = srow[min(lane, pos_t)];
+        sB = srow[min(kAttStep + lane, pos_t)];
+    }
+    auto add_sums = [&](uint32_t c, uint32_t par) {   // wavefront 4: the e of step c
+        const uint32_t p0 = c * kAttStep;
+        if (lane < 4 && st_t < ntok && pos0 + st_t >= p0) {
+            const uint32_t lim = min(kAttStep, pos0 + st_t + 1 - p0);
+            const float *e = eb + (par * 4 + stok) * kAttStep;
+            uint32_t r = 0;
+            for (; r + 4 <= lim; r += 4) {
+                const float4 e4 = *reinterpret_cast<const float4 *>(e + r);
+                sum += e4.x;
+                sum += e4.y;
+                sum += e4.z;
+                sum += e4.w;
+            }
+            for (; r < lim; r++) sum += e[r];
+        }
+    };
+    stream(std::true_type{}, [&](uint32_t c, const float *cur, auto parity) {
+        constexpr uint32_t par = decltype(parity)::value;
         const uint32_t p0 = c * kAttStep;
         if (w < 4) {
             if (!valid || pos_t < p0) return;
+            float *const e = eb + (par * 4 + tok) * kAttStep;
+            const uint32_t p = p0 + lane;
+            const float sv = par ? sB : sA;
+            const float ev = p <= pos_t ? pi_expf(sv - mx) : 0.0f;
+            e[lane] = ev;
+            const bool any_zero = __ballot(p <= pos_t && ev == 0.0f) != 0;
+            const float sn = srow[min(p + 2 * kAttStep, pos_t)];   // scores of step c + 2
+            if (par) sB = sn;
+            else sA = sn;
             const uint32_t lim = min(kAttStep, pos_t + 1 - p0);
-            const float *e = sct + p0, *vr = cur + lane * kVRow;
+            const float *vr = cur + lane * kVRow;
             uint32_t r = 0;
             auto four = [&](uint32_t q) {
                 const float4 e4 = *reinterpret_cast<const float4 *>(e + q);
@@ -733,7 +768,7 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                 acc = acc + e4.z * v4.z;
                 acc = acc + e4.w * v4.w;
             };
-            if (zflag[tok * nsteps + c] == 0u) {
+            if (!any_zero) {
                 if (lim == kAttStep) {
 #pragma unroll
                     for (uint32_t q = 0; q < kAttStep; q += 4) four(q);
@@ -746,21 +781,14 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                 const float ee = e[r];
                 acc = acc + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
             }
-        } else if (lane < 4 && st_t < ntok && pos0 + st_t >= p0) {
-            const uint32_t lim = min(kAttStep, pos0 + st_t + 1 - p0);
-            const float *e = sc + (uint64_t)stok * scs + p0;
-            uint32_t r = 0;
-            for (; r + 4 <= lim; r += 4) {
-                const float4 e4 = *reinterpret_cast<const float4 *>(e + r);
-                sum += e4.x;
-                sum += e4.y;
-                sum += e4.z;
-                sum += e4.w;
-            }
-            for (; r < lim; r++) sum += e[r];
+        } else if (c > 0) {
+            add_sums(c - 1, par ^ 1u);
         }
     });
-    if (w == 4 && lane < 4) misc[lane] = sum;
+    if (w == 4) {
+        add_sums(nsteps - 1, (nsteps - 1) & 1u);
+        if (lane < 4) misc[lane] = sum;
+    }
     __syncthreads();
     if (w < 4) {
         const float tot = misc[tok];
@@ -874,20 +902,12 @@ hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *
     return hipGetLastError();
 }
 
-size_t pi_pf_attn_lds_bytes(uint32_t n_ctx) {
-    const size_t nsteps = (n_ctx + kAttStep - 1) / kAttStep;
-    return (2 * (size_t)kAttBuf + 4 * 64 + 16 + 4 * ((nsteps + 3) & ~(size_t)3) + 4 * (((size_t)n_ctx + 3) & ~(size_t)3)) * 4;
-}
-
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
-                      uint32_t n_kv, uint32_t n_ctx, float scale, pi_pf_q8 o, hipStream_t s) {
+                      uint32_t n_kv, uint32_t n_ctx, float scale, float *scores, pi_pf_q8 o, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || pos0 + ntok > n_ctx || n_kv == 0 || n_head % n_kv) return hipErrorInvalidValue;
-    const size_t lds = pi_pf_attn_lds_bytes(n_ctx);
-    hipError_t e = hipFuncSetAttribute((const void *)k_pf_attn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
     const uint32_t blocks = 8 * ((ntok + 3) / 4) * ((n_head + 7) / 8);
-    hipLaunchKernelGGL(k_pf_attn, dim3(blocks), dim3(kAttThreads), lds, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
-                       n_ctx, scale, o.q, o.d, o.s);
+    hipLaunchKernelGGL(k_pf_attn, dim3(blocks), dim3(kAttThreads), 0, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
+                       n_ctx, scale, scores, o.q, o.d, o.s);
     return hipGetLastError();
 }
 
