@@ -569,62 +569,74 @@ __global__ __launch_bounds__(256) void k_pf_rope_kv(float *__restrict__ Q, const
 }
 
 // ---------------------------------------------------------------------------
-// Attention: a workgroup serves 4 tokens of one head with 5 wavefronts.  K,
-// then V, rows are staged through two LDS buffers 64 positions per step by
-// wavefronts 0-3, each step's rows loaded into registers two steps ahead
-// (one barrier per step).
-// Pass 1, scores (model.rs:1028-1038, scalar dot in d order, * scale):
-// wavefront t serves token t, lane = position; each score goes to the
+// Attention: a workgroup serves 4 * TPW consecutive tokens of one head with 5
+// wavefronts; wavefront w (0-3) serves tokens TPW*w..TPW*w+TPW-1 of them.
+// K, then V, rows are staged through two LDS buffers 64 positions per step
+// by wavefronts 0-3, each step's rows loaded into registers two steps ahead
+// (one barrier per step); every staged row feeds the chains of all the
+// workgroup's tokens.
+// Pass 1, scores (model.rs:1028-1038, scalar dot in d order, * scale): lane
+// = position, one chain per token of the wavefront; each score goes to the
 // token's row of a score scratch in global memory, and the maximum is kept.
-// Pass 2, per step: wavefront t reads its 64 scores back (loaded two steps
-// ahead), forms e_p = exp(s_p - max) lane-parallel into an LDS step buffer,
-// then adds e_p * v_p[d] in position order (f32_axpy order, model.rs:
-// 1056-1074: products rounded, e_p == 0 skipped), lane = dimension, from the
-// transposed V step; lane t of wavefront 4 adds sum += e_p of token t in
-// position order, one step behind.  V is staged as blocks of 4 positions x
-// 4 dimensions per thread, transposed in registers, so its LDS writes are
-// 16 bytes wide and free of bank conflicts.
+// Pass 2, per step: the wavefront reads its tokens' scores back (loaded two
+// steps ahead), forms e_p = exp(s_p - max) lane-parallel into an LDS step
+// buffer, then adds e_p * v_p[d] in position order (f32_axpy order,
+// model.rs:1056-1074: products rounded, e_p == 0 skipped), lane = dimension,
+// one chain per token, from the transposed V step; lane i of wavefront 4
+// adds sum += e_p of token i in position order, one step behind.  V is
+// staged as blocks of 4 positions x 4 dimensions per thread, transposed in
+// registers, so its LDS writes are 16 bytes wide and free of bank conflicts.
 // Output acc * (1/sum), then Q8 of the head's 64 values.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kAttStep = 64;               // positions per staged step
 constexpr uint32_t kAttThreads = 320;
+constexpr uint32_t kAttTpw = 2;                 // tokens per wavefront
+constexpr uint32_t kAttTok = 4 * kAttTpw;       // tokens per workgroup
 constexpr uint32_t kKRow = 68;                  // floats per staged K row
 constexpr uint32_t kVRow = kAttStep + 4;        // floats per staged transposed V row
 constexpr uint32_t kAttBuf = kAttStep * kKRow;  // floats per staging buffer (>= 64 * kVRow)
 static_assert(kAttBuf >= 64 * kVRow, "staging buffer holds a transposed V step");
-constexpr uint32_t kAttLdsFloats = 2 * kAttBuf + 4 * 64 + 2 * 4 * kAttStep + 16;
+static_assert(kAttTok <= 64, "wavefront 4 holds one token per lane");
 
+template <uint32_t TPW>
 __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
                                                          const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
                                                          uint32_t n_head, uint32_t group, uint32_t n_ctx, float scale,
                                                          float *__restrict__ scr, int8_t *__restrict__ oq,
                                                          float *__restrict__ od, int32_t *__restrict__ os) {
-    constexpr uint32_t DH = 64;
-    __shared__ __align__(16) float lds[kAttLdsFloats];
+    constexpr uint32_t DH = 64, TW = 4 * TPW;
+    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep + TW];
     float *const buf0 = lds, *const buf1 = lds + kAttBuf;
-    float *qs = lds + 2 * kAttBuf;              // 4 x 64
-    float *eb = qs + 4 * DH;                    // [2][4][64]: e of a step per token, two steps alternating
-    float *misc = eb + 2 * 4 * kAttStep;        // per-token sums
+    float *qs = lds + 2 * kAttBuf;              // [TW][64]
+    float *eb = qs + TW * DH;                   // [2][TW][64]: e of a step per token, two steps alternating
+    float *misc = eb + 2 * TW * kAttStep;       // per-token sums
     // Workgroup b runs on XCD b % 8 (round-robin dispatch): every workgroup of
     // head h gets b % 8 == h % 8, so a head's K/V rows are read into one L2.
-    const uint32_t ntg = (ntok + 3) / 4, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
+    const uint32_t ntg = (ntok + TW - 1) / TW, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
     const uint32_t tg = rest % ntg, h = (rest / ntg) * 8 + xcd;
     if (h >= n_head) return;   // before any barrier: the whole workgroup leaves
     const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
     const bool stager = w < 4;
-    const uint32_t tok = w & 3u;
-    const uint32_t t = 4 * tg + tok;
-    const bool valid = w < 4 && t < ntok;
-    const uint32_t pos_t = pos0 + t;
-    const uint32_t n_all = pos0 + min(4 * tg + 3, ntok - 1) + 1;
+    const uint32_t t0 = tg * TW + (w & 3u) * TPW;   // first token of this wavefront
+    const uint32_t n_all = pos0 + min(tg * TW + TW - 1, ntok - 1) + 1;
     const uint32_t nsteps = (n_all + kAttStep - 1) / kAttStep;
     const uint32_t kvh = h / group, qdim = n_head * DH;
     const float *kbase = kc + (uint64_t)kvh * n_ctx * DH, *vbase = vc + (uint64_t)kvh * n_ctx * DH;
-    // this token's scores; rows are whole 128-byte lines apart, so no other
-    // wavefront touches a line of this row
-    float *const srow = scr + ((uint64_t)min(t, ntok - 1) * n_head + h) * pi_pf_score_stride(n_ctx);
+    // tokens of this wavefront: valid ones are a prefix (consecutive tokens)
+    uint32_t nv = 0;
+    if (w < 4 && t0 < ntok) nv = min(TPW, ntok - t0);
+    const uint32_t pos_last = pos0 + t0 + (nv ? nv - 1 : 0);   // position of the wavefront's last valid token
+    // the tokens' scores; rows are whole 128-byte lines apart, so no other
+    // wavefront touches a line of these rows
+    auto srow = [&](uint32_t j) {
+        return scr + ((uint64_t)min(t0 + j, ntok - 1) * n_head + h) * pi_pf_score_stride(n_ctx);
+    };
 
-    if (w < 4) qs[tok * DH + lane] = t < ntok ? Q[(uint64_t)t * qdim + h * DH + lane] : 0.0f;
+    if (w < 4) {
+#pragma unroll
+        for (uint32_t j = 0; j < TPW; j++)
+            qs[((w & 3u) * TPW + j) * DH + lane] = j < nv ? Q[(uint64_t)(t0 + j) * qdim + h * DH + lane] : 0.0f;
+    }
 
     struct Rows {
         float4 v[4];
@@ -694,44 +706,65 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
         }
     };
 
-    // ---- pass 1: scores and maximum -------------------------------------
-    float mx = -INFINITY;
+    // ---- pass 1: scores and maxima -----------------------------------------
+    float mx[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) mx[j] = -INFINITY;
     stream(std::false_type{}, [&](uint32_t c, const float *cur, auto) {
         const uint32_t p = c * kAttStep + lane;
-        if (valid && p <= pos_t) {
+        if (nv && p <= pos_last) {
             const float4 *kr = reinterpret_cast<const float4 *>(cur + lane * kKRow);
-            const float4 *q4 = reinterpret_cast<const float4 *>(qs + tok * DH);
-            float s = 0.0f;
+            float sc[TPW];
 #pragma unroll
+            for (uint32_t j = 0; j < TPW; j++) sc[j] = 0.0f;
+#pragma unroll 4
             for (int d4 = 0; d4 < 16; d4++) {
-                const float4 kk = kr[d4], qq = q4[d4];
-                s += qq.x * kk.x;
-                s += qq.y * kk.y;
-                s += qq.z * kk.z;
-                s += qq.w * kk.w;
+                const float4 kk = kr[d4];
+#pragma unroll
+                for (uint32_t j = 0; j < TPW; j++) {
+                    const float4 qq = reinterpret_cast<const float4 *>(qs + ((w & 3u) * TPW + j) * DH)[d4];
+                    sc[j] += qq.x * kk.x;
+                    sc[j] += qq.y * kk.y;
+                    sc[j] += qq.z * kk.z;
+                    sc[j] += qq.w * kk.w;
+                }
             }
-            s = s * scale;
-            srow[p] = s;
-            mx = fmaxf(mx, s);
+#pragma unroll
+            for (uint32_t j = 0; j < TPW; j++) {
+                if (j < nv && p <= pos0 + t0 + j) {
+                    const float sv = sc[j] * scale;
+                    srow(j)[p] = sv;
+                    mx[j] = fmaxf(mx[j], sv);
+                }
+            }
         }
     });
 #pragma unroll
-    for (int off = 32; off; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    for (uint32_t j = 0; j < TPW; j++)
+#pragma unroll
+        for (int off = 32; off; off >>= 1) mx[j] = fmaxf(mx[j], __shfl_xor(mx[j], off, 64));
 
     // ---- pass 2: e, then the sums in position order --------------------------
-    float acc = 0.0f, sum = 0.0f;
-    const uint32_t stok = lane & 3u, st_t = 4 * tg + stok;   // wavefront 4: lane = token
+    float acc[TPW], sum = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) acc[j] = 0.0f;
+    const uint32_t st_t = tg * TW + lane;   // wavefront 4: lane = token
     // scores of steps 0 and 1 (this lane's position, clamped to written ones)
-    float sA = 0.0f, sB = 0.0f;
-    if (valid) {
-        sA = srow[min(lane, pos_t)];
-        sB = srow[min(kAttStep + lane, pos_t)];
+    float sA[TPW], sB[TPW];
+#pragma unroll
+    for (uint32_t j = 0; j < TPW; j++) {
+        sA[j] = sB[j] = 0.0f;
+        if (j < nv) {
+            const uint32_t pj = pos0 + t0 + j;
+            sA[j] = srow(j)[min(lane, pj)];
+            sB[j] = srow(j)[min(kAttStep + lane, pj)];
+        }
     }
     auto add_sums = [&](uint32_t c, uint32_t par) {   // wavefront 4: the e of step c
         const uint32_t p0 = c * kAttStep;
-        if (lane < 4 && st_t < ntok && pos0 + st_t >= p0) {
+        if (lane < TW && st_t < ntok && pos0 + st_t >= p0) {
             const uint32_t lim = min(kAttStep, pos0 + st_t + 1 - p0);
-            const float *e = eb + (par * 4 + stok) * kAttStep;
+            const float *e = eb + (par * TW + lane) * kAttStep;
             uint32_t r = 0;
             for (; r + 4 <= lim; r += 4) {
                 const float4 e4 = *reinterpret_cast<const float4 *>(e + r);
@@ -747,39 +780,49 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
         constexpr uint32_t par = decltype(parity)::value;
         const uint32_t p0 = c * kAttStep;
         if (w < 4) {
-            if (!valid || pos_t < p0) return;
-            float *const e = eb + (par * 4 + tok) * kAttStep;
+            if (nv == 0 || pos_last < p0) return;
             const uint32_t p = p0 + lane;
-            const float sv = par ? sB : sA;
-            const float ev = p <= pos_t ? pi_expf(sv - mx) : 0.0f;
-            e[lane] = ev;
-            const bool any_zero = __ballot(p <= pos_t && ev == 0.0f) != 0;
-            const float sn = srow[min(p + 2 * kAttStep, pos_t)];   // scores of step c + 2
-            if (par) sB = sn;
-            else sA = sn;
-            const uint32_t lim = min(kAttStep, pos_t + 1 - p0);
-            const float *vr = cur + lane * kVRow;
-            uint32_t r = 0;
-            auto four = [&](uint32_t q) {
-                const float4 e4 = *reinterpret_cast<const float4 *>(e + q);
-                const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
-                acc = acc + e4.x * v4.x;
-                acc = acc + e4.y * v4.y;
-                acc = acc + e4.z * v4.z;
-                acc = acc + e4.w * v4.w;
-            };
-            if (!any_zero) {
-                if (lim == kAttStep) {
+            float *const e0 = eb + (par * TW + (w & 3u) * TPW) * kAttStep;   // [TPW][64]
+            bool slow = false;   // a token ends inside this step or has an e_p == 0 in it
 #pragma unroll
-                    for (uint32_t q = 0; q < kAttStep; q += 4) four(q);
-                    r = kAttStep;
-                } else {
-                    for (; r + 4 <= lim; r += 4) four(r);
-                }
+            for (uint32_t j = 0; j < TPW; j++) {
+                const uint32_t pj = pos0 + t0 + j;
+                const float sv = par ? sB[j] : sA[j];
+                const bool in = j < nv && p <= pj;
+                const float ev = in ? pi_expf(sv - mx[j]) : 0.0f;
+                e0[j * kAttStep + lane] = ev;
+                slow |= __ballot(in && ev == 0.0f) != 0;
+                slow |= j >= nv || pj < p0 + kAttStep - 1;
+                const float sn = j < nv ? srow(j)[min(p + 2 * kAttStep, pj)] : 0.0f;   // scores of step c + 2
+                if (par) sB[j] = sn;
+                else sA[j] = sn;
             }
-            for (; r < lim; r++) {
-                const float ee = e[r];
-                acc = acc + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
+            const float *vr = cur + lane * kVRow;
+            if (!slow) {
+#pragma unroll
+                for (uint32_t q = 0; q < kAttStep; q += 4) {
+                    const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
+#pragma unroll
+                    for (uint32_t j = 0; j < TPW; j++) {
+                        const float4 e4 = *reinterpret_cast<const float4 *>(e0 + j * kAttStep + q);
+                        acc[j] = acc[j] + e4.x * v4.x;
+                        acc[j] = acc[j] + e4.y * v4.y;
+                        acc[j] = acc[j] + e4.z * v4.z;
+                        acc[j] = acc[j] + e4.w * v4.w;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (uint32_t j = 0; j < TPW; j++) {
+                    const uint32_t pj = pos0 + t0 + j;
+                    if (j >= nv || pj < p0) continue;
+                    const uint32_t lim = min(kAttStep, pj + 1 - p0);
+                    const float *e = e0 + j * kAttStep;
+                    for (uint32_t r = 0; r < lim; r++) {
+                        const float ee = e[r];
+                        acc[j] = acc[j] + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
+                    }
+                }
             }
         } else if (c > 0) {
             add_sums(c - 1, par ^ 1u);
@@ -787,22 +830,25 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
     });
     if (w == 4) {
         add_sums(nsteps - 1, (nsteps - 1) & 1u);
-        if (lane < 4) misc[lane] = sum;
+        if (lane < TW) misc[lane] = sum;
     }
     __syncthreads();
     if (w < 4) {
-        const float tot = misc[tok];
-        const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
-        const float o = acc * inv;
-        const uint32_t blk = h * 2 + lane / 32, j = lane % 32;
-        float dd;
-        int sum;
-        const int iv = q8_block32_core(o, dd, sum);
-        if (valid) {
-            oq[pfq_off(blk, j / 8, t) + j % 8] = (int8_t)iv;
-            if (j == 0) {
-                od[blk * PI_PF_MAX_TOK + t] = dd;
-                os[blk * PI_PF_MAX_TOK + t] = sum;
+#pragma unroll
+        for (uint32_t j = 0; j < TPW; j++) {
+            const float tot = misc[(w & 3u) * TPW + j];
+            const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
+            const float o = acc[j] * inv;
+            const uint32_t blk = h * 2 + lane / 32, jj = lane % 32, t = t0 + j;
+            float dd;
+            int bsum;
+            const int iv = q8_block32_core(o, dd, bsum);
+            if (j < nv) {
+                oq[pfq_off(blk, jj / 8, t) + jj % 8] = (int8_t)iv;
+                if (jj == 0) {
+                    od[blk * PI_PF_MAX_TOK + t] = dd;
+                    os[blk * PI_PF_MAX_TOK + t] = bsum;
+                }
             }
         }
     }
@@ -905,8 +951,8 @@ hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
                       uint32_t n_kv, uint32_t n_ctx, float scale, float *scores, pi_pf_q8 o, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || pos0 + ntok > n_ctx || n_kv == 0 || n_head % n_kv) return hipErrorInvalidValue;
-    const uint32_t blocks = 8 * ((ntok + 3) / 4) * ((n_head + 7) / 8);
-    hipLaunchKernelGGL(k_pf_attn, dim3(blocks), dim3(kAttThreads), 0, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
+    const uint32_t blocks = 8 * ((ntok + kAttTok - 1) / kAttTok) * ((n_head + 7) / 8);
+    hipLaunchKernelGGL(k_pf_attn<kAttTpw>, dim3(blocks), dim3(kAttThreads), 0, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
                        n_ctx, scale, scores, o.q, o.d, o.s);
     return hipGetLastError();
 }
