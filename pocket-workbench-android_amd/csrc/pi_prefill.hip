@@ -136,7 +136,7 @@ struct PfLds<PI_TYPE_Q8_0> {
 // round are issued before any is used).
 template <uint32_t T>
 __device__ __forceinline__ void decode_consts(const WV &W, uint32_t r0, uint32_t nb, float *cst) {
-    constexpr uint32_t R = (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) ? 2u : 24u;   // entries per thread per round
+    constexpr uint32_t R = (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) ? 2u : 12u;   // entries per thread per round
     const uint32_t tid = threadIdx.x, ne = nb * kPfRows;
     for (uint32_t base = 0; base < ne; base += kPfThreads * R) {
         if constexpr (T == PI_TYPE_Q4_K || T == PI_TYPE_Q6_K) {
@@ -240,7 +240,7 @@ struct TermAct {
 };
 
 template <uint32_t T>
-__global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *__restrict__ aq,
+__global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4))) void k_pf_gemm(PfSegs S, const int8_t *__restrict__ aq,
                                                          const float *__restrict__ ad, const int32_t *__restrict__ as,
                                                          uint32_t k, uint32_t ntok, int resid) {
     using ST = PfStage<T>;
@@ -403,6 +403,11 @@ __global__ __launch_bounds__(kPfThreads) void k_pf_gemm(PfSegs S, const int8_t *
         X = load_act(tg + kPfActDepth);
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i] = acc[i] + t[i];
+        // Q6_K, Q8_0, Q4_0: the sums are pinned after each term, which keeps
+        // the compiler from forming all 16 MFMAs of a phase ahead of their
+        // terms (4 more wavefronts per SIMD fit); Q4_K runs faster with them
+        // formed ahead within its 128-register budget.
+        if constexpr (T != PI_TYPE_Q4_K) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
     };
     for (uint32_t ph = 0; ph < nph; ph++) {
         const uint4 *wb = (ph & 1u) ? wb1 : wb0;
