@@ -403,11 +403,11 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         X = load_act(tg + kPfActDepth);
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i] = acc[i] + t[i];
-        // Q6_K, Q8_0, Q4_0: the sums are pinned after each term, which keeps
-        // the compiler from forming all 16 MFMAs of a phase ahead of their
-        // terms (4 more wavefronts per SIMD fit); Q4_K runs faster with them
-        // formed ahead within its 128-register budget.
-        if constexpr (T != PI_TYPE_Q4_K) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+        // Q6_K, Q8_0: the sums are pinned after each term, which keeps the
+        // compiler from forming all 16 MFMAs of a phase ahead of their terms
+        // (more wavefronts per SIMD fit); Q4_K and Q4_0 run faster with them
+        // formed ahead within the 128-register budget (measured).
+        if constexpr (T != PI_TYPE_Q4_K && T != PI_TYPE_Q4_0) asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
     };
     for (uint32_t ph = 0; ph < nph; ph++) {
         const uint4 *wb = (ph & 1u) ? wb1 : wb0;
