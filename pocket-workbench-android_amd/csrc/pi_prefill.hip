@@ -610,11 +610,12 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                                                          float *__restrict__ scr, int8_t *__restrict__ oq,
                                                          float *__restrict__ od, int32_t *__restrict__ os) {
     constexpr uint32_t DH = 64, TW = 4 * TPW;
-    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep + TW];
+    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep + TW + 8];
     float *const buf0 = lds, *const buf1 = lds + kAttBuf;
     float *qs = lds + 2 * kAttBuf;              // [TW][64]
     float *eb = qs + TW * DH;                   // [2][TW][64]: e of a step per token, two steps alternating
     float *misc = eb + 2 * TW * kAttStep;       // per-token sums
+    uint32_t *vbad = reinterpret_cast<uint32_t *>(misc + TW);   // [2][4]: a staging wavefront saw a non-finite V
     // Workgroup b runs on XCD b % 8 (round-robin dispatch): every workgroup of
     // head h gets b % 8 == h % 8, so a head's K/V rows are read into one L2.
     const uint32_t ntg = (ntok + TW - 1) / TW, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
@@ -681,6 +682,13 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
         *reinterpret_cast<float4 *>(d0 + kVRow) = make_float4(R.v[0].y, R.v[1].y, R.v[2].y, R.v[3].y);
         *reinterpret_cast<float4 *>(d0 + 2 * kVRow) = make_float4(R.v[0].z, R.v[1].z, R.v[2].z, R.v[3].z);
         *reinterpret_cast<float4 *>(d0 + 3 * kVRow) = make_float4(R.v[0].w, R.v[1].w, R.v[2].w, R.v[3].w);
+        bool fin = true;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            fin = fin && __builtin_isfinite(R.v[j].x) && __builtin_isfinite(R.v[j].y) &&
+                  __builtin_isfinite(R.v[j].z) && __builtin_isfinite(R.v[j].w);
+        const bool bad = __ballot(!fin) != 0;
+        if (lane == 0) vbad[(bf == buf1 ? 4u : 0u) + w] = bad ? 1u : 0u;
     };
     // Runs body(c, buffer of step c, parity of c) for every step; rows of step
     // c + 1 are stored while step c is used, rows of step c + 2 are in flight.
@@ -788,7 +796,11 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
             if (nv == 0 || pos_last < p0) return;
             const uint32_t p = p0 + lane;
             float *const e0 = eb + (par * TW + (w & 3u) * TPW) * kAttStep;   // [TPW][64]
-            bool slow = false;   // a token ends inside this step or has an e_p == 0 in it
+            // Skipping a position with e_p == 0 leaves the sum as adding
+            // e_p * v = +-0 would (the sum starts at +0, so it is never -0),
+            // unless v is infinite or NaN: the skip is taken only in a step
+            // whose staged V holds such a value.
+            bool zero = false, full = true;
 #pragma unroll
             for (uint32_t j = 0; j < TPW; j++) {
                 const uint32_t pj = pos0 + t0 + j;
@@ -796,14 +808,16 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                 const bool in = j < nv && p <= pj;
                 const float ev = in ? pi_expf(sv - mx[j]) : 0.0f;
                 e0[j * kAttStep + lane] = ev;
-                slow |= __ballot(in && ev == 0.0f) != 0;
-                slow |= j >= nv || pj < p0 + kAttStep - 1;
+                zero |= __ballot(in && ev == 0.0f) != 0;
+                full &= j < nv && pj >= p0 + kAttStep - 1;
                 const float sn = j < nv ? srow(j)[min(p + 2 * kAttStep, pj)] : 0.0f;   // scores of step c + 2
                 if (par) sB[j] = sn;
                 else sA[j] = sn;
             }
+            const uint32_t *vb = vbad + par * 4u;
+            const bool skip = zero && (vb[0] | vb[1] | vb[2] | vb[3]) != 0u;
             const float *vr = cur + lane * kVRow;
-            if (!slow) {
+            if (full && !skip) {
 #pragma unroll
                 for (uint32_t q = 0; q < kAttStep; q += 4) {
                     const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
@@ -823,9 +837,22 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                     if (j >= nv || pj < p0) continue;
                     const uint32_t lim = min(kAttStep, pj + 1 - p0);
                     const float *e = e0 + j * kAttStep;
-                    for (uint32_t r = 0; r < lim; r++) {
-                        const float ee = e[r];
-                        acc[j] = acc[j] + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
+                    uint32_t r = 0;
+                    if (!skip) {
+                        for (; r + 4 <= lim; r += 4) {
+                            const float4 e4 = *reinterpret_cast<const float4 *>(e + r);
+                            const float4 v4 = *reinterpret_cast<const float4 *>(vr + r);
+                            acc[j] = acc[j] + e4.x * v4.x;
+                            acc[j] = acc[j] + e4.y * v4.y;
+                            acc[j] = acc[j] + e4.z * v4.z;
+                            acc[j] = acc[j] + e4.w * v4.w;
+                        }
+                        for (; r < lim; r++) acc[j] = acc[j] + e[r] * vr[r];
+                    } else {
+                        for (; r < lim; r++) {
+                            const float ee = e[r];
+                            acc[j] = acc[j] + (ee != 0.0f ? ee * vr[r] : -0.0f);   // x + (-0) == x: a skipped position
+                        }
                     }
                 }
             }

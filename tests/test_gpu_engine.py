@@ -128,6 +128,41 @@ def test_tiny_generate_passes_span_chunks(pih, backend, oracle, tiny, n_prompt):
     assert _bits_equal(eng.logits(), ref.logits())
 
 
+def test_tiny_attention_skips_zero_weights(pih, backend, oracle, tiny):
+    """model.rs:1048-1069 adds e_p * v_p only where e_p != 0.  The cache rows
+    of positions 0..63 are set so that one position takes every weight: K is
+    zero except +-1e6 * u at positions 10 and 37, so one of them holds a score
+    of order 1e5 and every other e_p is exp(-1e5) == 0; the V rows of the
+    other positions hold inf, -inf and NaN.  Skipping them leaves finite
+    outputs (adding 0 * inf would not).  Logits of a batched forward and of
+    the next single token equal the oracle's bit for bit."""
+    s = tiny.spec
+    eng = pih.HipEngine(backend, tiny, n_ctx=128)
+    ref = oracle.OracleEngine(tiny, n_ctx=128, threads=4)
+    rk, rv = ref.kv()
+    rng = np.random.default_rng(5)
+    npos = 64
+    u = rng.standard_normal(s.head_dim).astype(np.float32)
+    for layer in range(s.n_layer):
+        for h in range(s.n_head_kv):
+            k = np.zeros((npos, s.head_dim), np.float32)
+            k[10], k[37] = 1e6 * u, -1e6 * u
+            v = rng.standard_normal((npos, s.head_dim)).astype(np.float32)
+            for i, p in enumerate(p for p in range(npos) if p not in (10, 37) and p % 3 == 0):
+                v[p, (7 * i) % s.head_dim] = (np.inf, -np.inf, np.nan)[i % 3]
+            eng.kv_write(layer, h, 0, k, v)
+            rk[layer, h, :npos], rv[layer, h, :npos] = k, v
+    ids = list(range(100, 108))
+    eng.forward(ids, list(range(npos, npos + 8)), want_logits=True)
+    ref.forward(ids, list(range(npos, npos + 8)), want_logits=True)
+    want = ref.logits()
+    assert np.isfinite(want).all()
+    assert _bits_equal(eng.logits(), want)
+    eng.forward([7], [npos + 8], want_logits=True)
+    ref.forward([7], [npos + 8], want_logits=True)
+    assert _bits_equal(eng.logits(), ref.logits())
+
+
 def test_tiny_prefix_reuse(pih, backend, oracle, tiny):
     """tests/prefix_cache.rs:27-63 invariants on the device engine.  A context
     holds one engine, so the fresh run comes first."""
