@@ -117,7 +117,7 @@ struct Engine {
     size_t mega_lds = 0;
     // batched prefill (pi_prefill.hip): token-major chunk buffers
     bool pf_ok = false;
-    float *pfX = nullptr, *pfQ = nullptr, *pfK = nullptr, *pfV = nullptr, *pfG = nullptr, *pfU = nullptr;
+    float *pfX = nullptr, *pfQ = nullptr, *pfG = nullptr, *pfU = nullptr;
     float *pfS = nullptr;   // attention scores of a pass: [token][head][n_ctx]
     int8_t *pfq = nullptr;
     float *pfd = nullptr;
@@ -329,7 +329,7 @@ void engine_free(Engine *e) {
     for (void *p : {(void *)e->mega_dev, (void *)e->mega_layers, (void *)e->mega_words, (void *)e->mega_part,
                     (void *)e->mega_abort, (void *)e->mega_trace, (void *)e->mega_amax, (void *)e->mega_aexp})
         dfree(p);
-    for (void *p : {(void *)e->pfX, (void *)e->pfQ, (void *)e->pfK, (void *)e->pfV, (void *)e->pfG, (void *)e->pfU,
+    for (void *p : {(void *)e->pfX, (void *)e->pfQ, (void *)e->pfG, (void *)e->pfU,
                     (void *)e->pfS, (void *)e->pfq, (void *)e->pfd, (void *)e->pfs, (void *)e->pf_ids})
         dfree(p);
     for (void *p : {(void *)e->embd, (void *)e->out_norm, (void *)e->kc, (void *)e->vc, (void *)e->cos_tab,
@@ -608,13 +608,13 @@ bool use_mega(const pi_ctx *c, const Engine &e) { return c->use_persistent && e.
 // one by one) when the model is outside the kernels' limits.
 int build_prefill(pi_ctx *c, Engine &e) {
     e.pf_ok = false;
-    const uint32_t qdim = e.n_head * e.dh, kdim = e.n_kv * e.dh;
+    const uint32_t qdim = e.n_head * e.dh;
     if (e.dh != 64 || e.n_embd / 32 > 256 || e.n_rot / 2 > 32) return PI_OK;
     const uint64_t T = PI_PF_MAX_TOK;
     const uint64_t kmax = std::max(std::max(e.n_embd, e.n_ff), qdim);
     int r;
-    if ((r = dalloc(c, &e.pfX, T * e.n_embd)) || (r = dalloc(c, &e.pfQ, T * qdim)) || (r = dalloc(c, &e.pfK, T * kdim)) ||
-        (r = dalloc(c, &e.pfV, T * kdim)) || (r = dalloc(c, &e.pfG, T * e.n_ff)) || (r = dalloc(c, &e.pfU, T * e.n_ff)) ||
+    if ((r = dalloc(c, &e.pfX, T * e.n_embd)) || (r = dalloc(c, &e.pfQ, T * qdim)) ||
+        (r = dalloc(c, &e.pfG, T * e.n_ff)) || (r = dalloc(c, &e.pfU, T * e.n_ff)) ||
         (r = dalloc(c, &e.pfq, T * kmax)) || (r = dalloc(c, &e.pfd, T * kmax / 32)) || (r = dalloc(c, &e.pfs, T * kmax / 32)) ||
         (r = dalloc(c, &e.pfS, T * e.n_head * pi_pf_score_stride(e.n_ctx))) || (r = dalloc(c, &e.pf_ids, 2 * T)))
         return r;
@@ -642,18 +642,28 @@ hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, u
         float *vc = e.vc + (uint64_t)l * e.n_kv * e.n_ctx * e.dh;
         K(pi_pf_norm_q8(e.pfX, L.attn_norm, e.n_embd, e.eps, ntok, A, s));
         {
+            // Q, K, V with RoPE and the cache rows of positions pos0.. formed
+            // in the GEMM's epilogue (matrices of one type share a launch)
+            const pi_pf_rope rp{e.cos_tab, e.sin_tab, pos0, e.n_rot / 2, e.n_ctx};
             const pi_pf_mat m[3] = {pfmat(L.q), pfmat(L.k), pfmat(L.v)};
-            float *const o[3] = {e.pfQ, e.pfK, e.pfV};
-            if (m[2].L.type == m[0].L.type && m[1].L.type == m[0].L.type) {
-                K(pi_pf_gemm_multi(m, o, 3, A, ntok, false, s));
-            } else {
-                K(pi_pf_gemm_multi(m, o, m[1].L.type == m[0].L.type ? 2 : 1, A, ntok, false, s));
-                if (m[1].L.type != m[0].L.type) K(pi_pf_gemm(m[1], A, ntok, e.pfK, false, s));
-                K(pi_pf_gemm(m[2], A, ntok, e.pfV, false, s));
+            float *const o[3] = {e.pfQ, kc, vc};
+            const uint32_t md[3] = {PI_PF_ROPE, PI_PF_ROPE_CACHE, PI_PF_CACHE};
+            bool done[3] = {false, false, false};
+            for (uint32_t i = 0; i < 3; i++) {
+                if (done[i]) continue;
+                pi_pf_mat gm[3];
+                float *go[3];
+                uint32_t gmd[3], n = 0;
+                for (uint32_t j = i; j < 3; j++) {
+                    if (done[j] || m[j].L.type != m[i].L.type || m[j].L.k != m[i].L.k) continue;
+                    gm[n] = m[j];
+                    go[n] = o[j];
+                    gmd[n++] = md[j];
+                    done[j] = true;
+                }
+                K(pi_pf_gemm_multi(gm, go, gmd, n, A, ntok, false, &rp, s));
             }
         }
-        K(pi_pf_rope_kv(e.pfQ, e.pfK, e.pfV, e.cos_tab, e.sin_tab, pos0, ntok, e.n_head, e.n_kv, e.n_rot / 2, kc, vc,
-                        e.n_ctx, s));
         K(pi_pf_attn(e.pfQ, kc, vc, pos0, ntok, e.n_head, e.n_kv, e.n_ctx, scale, e.pfS, A, s));
         K(pi_pf_gemm(pfmat(L.o), A, ntok, e.pfX, true, s));
         K(pi_pf_norm_q8(e.pfX, L.ffn_norm, e.n_embd, e.eps, ntok, A, s));
@@ -661,7 +671,7 @@ hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, u
             const pi_pf_mat m[2] = {pfmat(L.gate), pfmat(L.up)};
             float *const o[2] = {e.pfG, e.pfU};
             if (m[1].L.type == m[0].L.type) {
-                K(pi_pf_gemm_multi(m, o, 2, A, ntok, false, s));
+                K(pi_pf_gemm_multi(m, o, nullptr, 2, A, ntok, false, nullptr, s));
             } else {
                 K(pi_pf_gemm(m[0], A, ntok, e.pfG, false, s));
                 K(pi_pf_gemm(m[1], A, ntok, e.pfU, false, s));

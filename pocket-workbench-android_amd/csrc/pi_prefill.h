@@ -40,15 +40,21 @@ hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps,
 // sums of every 32- (Q6_K: 16-) element group, the reference's float
 // epilogue in block order per (row, token).
 hipError_t pi_pf_gemm(const pi_pf_mat &W, pi_pf_q8 act, uint32_t ntok, float *out, bool resid, hipStream_t s);
+// What the GEMM does with an output of 64-dimension heads (rows a multiple
+// of 64) instead of storing it: RoPE of its pairs (model.rs:953-979) into a
+// token-major matrix (Q), RoPE then the rows of positions pos0..pos0+ntok-1
+// of a [head][n_ctx][64] cache (K, 984-992), or the cache rows alone (V).
+enum pi_pf_out : uint32_t { PI_PF_STORE = 0, PI_PF_ROPE = 1, PI_PF_ROPE_CACHE = 2, PI_PF_CACHE = 3 };
+struct pi_pf_rope {
+    const float *cos_tab, *sin_tab;   // [n_ctx][half]
+    uint32_t pos0, half, n_ctx;
+};
 // The same for up to 3 matrices of one type and row length sharing the
-// activation, in one launch; out[i] is a [ntok][rows of M[i]] matrix.
-hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg, pi_pf_q8 act, uint32_t ntok,
-                            bool resid, hipStream_t s);
-// RoPE of Q and K of every token (model.rs:953-979) and the K/V rows of
-// positions pos0..pos0+ntok-1 written into this layer's caches (984-992).
-hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *cos_tab, const float *sin_tab,
-                         uint32_t pos0, uint32_t ntok, uint32_t n_head, uint32_t n_kv, uint32_t half, float *kc,
-                         float *vc, uint32_t n_ctx, hipStream_t s);
+// activation, in one launch; out[i] is a [ntok][rows of M[i]] matrix, or the
+// layer's cache for the cache modes (mode = nullptr: all PI_PF_STORE; the
+// other modes need rope and resid == false).
+hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, const uint32_t *mode, uint32_t nseg, pi_pf_q8 act,
+                            uint32_t ntok, bool resid, const pi_pf_rope *rope, hipStream_t s);
 // Attention of every token over positions 0..its own (model.rs:993-1087,
 // multi-token orders), then Q8 of the output.  scores: scratch of
 // PI_PF_MAX_TOK * n_head * pi_pf_score_stride(n_ctx) floats.

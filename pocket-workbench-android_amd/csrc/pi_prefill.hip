@@ -91,7 +91,9 @@ struct PfSegs {
     WV W[kPfMaxSeg];
     float *out[kPfMaxSeg];
     uint32_t wg_end[kPfMaxSeg];   // cumulative workgroup counts
+    uint32_t mode[kPfMaxSeg];     // pi_pf_out
     uint32_t nseg;
+    pi_pf_rope rope;
 };
 
 // Offset of the 8 quants 8*ka..+7 of group G of token t in a prefill Q8 buffer.
@@ -251,6 +253,7 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
     const uint32_t seg = (S.nseg > 1 && wg >= S.wg_end[0]) ? ((S.nseg > 2 && wg >= S.wg_end[1]) ? 2u : 1u) : 0u;
     const WV W = seg == 0 ? S.W[0] : (seg == 1 ? S.W[1] : S.W[2]);
     float *const out = seg == 0 ? S.out[0] : (seg == 1 ? S.out[1] : S.out[2]);
+    const uint32_t mode = seg == 0 ? S.mode[0] : (seg == 1 ? S.mode[1] : S.mode[2]);
     const uint32_t wg0 = seg == 0 ? 0u : (seg == 1 ? S.wg_end[0] : S.wg_end[1]);
     const uint32_t ntb = (ntok + kPfTokWg - 1) / kPfTokWg;
     const uint32_t rg = (wg - wg0) / ntb, tb = (wg - wg0) - rg * ntb;
@@ -424,17 +427,41 @@ __global__ __launch_bounds__(kPfThreads) __attribute__((amdgpu_waves_per_eu(4)))
         SW = load_pieces(min(ph + 2, nph - 1));
         __syncthreads();
     }
-    if (n < ntok) {
+    if (n >= ntok) return;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = 0.0f + acc[i];
+    if (mode == PI_PF_STORE) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t r = r0 + 4 * ka + i;
             if (r < W.rows) {
                 float *o = out + (uint64_t)n * W.rows + r;
-                const float v = 0.0f + acc[i];
-                *o = resid ? *o + v : v;
+                *o = resid ? *o + v[i] : v[i];
+            }
+        }
+        return;
+    }
+    // Rows of 64-dimension heads (rows a multiple of 64): this lane holds
+    // dimensions d..d+3 of head rr / 64 for token n at position pos.
+    const uint32_t rr = r0 + 4 * ka, d = rr % 64, pos = S.rope.pos0 + n;
+    if (mode != PI_PF_CACHE) {
+        // RoPE of the pairs (d, d+1), (d+2, d+3) (model.rs:953-979)
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const uint32_t p = d / 2 + q;
+            if (p < S.rope.half) {
+                const float c = S.rope.cos_tab[(uint64_t)pos * S.rope.half + p];
+                const float sn = S.rope.sin_tab[(uint64_t)pos * S.rope.half + p];
+                const float x0 = v[2 * q], x1 = v[2 * q + 1];
+                v[2 * q] = x0 * c - x1 * sn;
+                v[2 * q + 1] = x0 * sn + x1 * c;
             }
         }
     }
+    float *o = mode == PI_PF_ROPE ? out + (uint64_t)n * W.rows + rr
+                                  : out + ((uint64_t)(rr / 64) * S.rope.n_ctx + pos) * 64 + d;   // cache row (984-992)
+    *reinterpret_cast<float4 *>(o) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
 // ---------------------------------------------------------------------------
@@ -530,47 +557,6 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ 
     int sum;
     q8_pair_core(v, w4, dd, sum);
     pf_store_pair(o, t, b, hh, w4, dd, sum);
-}
-
-// ---------------------------------------------------------------------------
-// RoPE + KV rows (one token per workgroup).
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_pf_rope_kv(float *__restrict__ Q, const float *__restrict__ K,
-                                                    const float *__restrict__ V, const float *__restrict__ cos_tab,
-                                                    const float *__restrict__ sin_tab, uint32_t pos0,
-                                                    uint32_t n_head, uint32_t n_kv, uint32_t half,
-                                                    float *__restrict__ kc, float *__restrict__ vc, uint32_t n_ctx) {
-    constexpr uint32_t DH = 64;
-    const uint32_t t = blockIdx.x, pos = pos0 + t;
-    const float *cb = cos_tab + (uint64_t)pos * half, *sb = sin_tab + (uint64_t)pos * half;
-    const uint32_t qdim = n_head * DH, kdim = n_kv * DH;
-    for (uint32_t i = threadIdx.x; i < n_head * (DH / 2); i += blockDim.x) {
-        const uint32_t h = i / (DH / 2), p = i % (DH / 2);
-        if (p < half) {
-            float *x = Q + (uint64_t)t * qdim + h * DH + 2 * p;
-            const float x0 = x[0], x1 = x[1], c = cb[p], s = sb[p];
-            x[0] = x0 * c - x1 * s;
-            x[1] = x0 * s + x1 * c;
-        }
-    }
-    for (uint32_t i = threadIdx.x; i < n_kv * (DH / 2); i += blockDim.x) {
-        const uint32_t h = i / (DH / 2), p = i % (DH / 2);
-        const float *x = K + (uint64_t)t * kdim + h * DH + 2 * p;
-        float y0 = x[0], y1 = x[1];
-        if (p < half) {
-            const float c = cb[p], s = sb[p];
-            const float r0 = y0 * c - y1 * s, r1 = y0 * s + y1 * c;
-            y0 = r0;
-            y1 = r1;
-        }
-        float *dst = kc + ((uint64_t)h * n_ctx + pos) * DH + 2 * p;
-        dst[0] = y0;
-        dst[1] = y1;
-    }
-    for (uint32_t i = threadIdx.x; i < kdim; i += blockDim.x) {
-        const uint32_t h = i / DH, dd = i % DH;
-        vc[((uint64_t)h * n_ctx + pos) * DH + dd] = V[(uint64_t)t * kdim + i];
-    }
 }
 
 // ---------------------------------------------------------------------------
@@ -917,14 +903,20 @@ hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps,
     return hipGetLastError();
 }
 
-hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg, pi_pf_q8 a, uint32_t ntok,
-                             bool resid, hipStream_t s) {
+hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, const uint32_t *mode, uint32_t nseg, pi_pf_q8 a,
+                             uint32_t ntok, bool resid, const pi_pf_rope *rope, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || nseg == 0 || nseg > kPfMaxSeg) return hipErrorInvalidValue;
     const uint32_t t = M[0].L.type, k = M[0].L.k;
     PfSegs S{};
+    if (rope) S.rope = *rope;
     uint32_t wgs = 0;
     for (uint32_t i = 0; i < nseg; i++) {
         if (M[i].L.type != t || M[i].L.k != k || M[i].L.rows == 0) return hipErrorInvalidValue;
+        S.mode[i] = mode ? mode[i] : PI_PF_STORE;
+        if (S.mode[i] > PI_PF_CACHE) return hipErrorInvalidValue;
+        if (S.mode[i] != PI_PF_STORE &&
+            (resid || !rope || M[i].L.rows % 64 || rope->half > 32 || rope->pos0 + ntok > rope->n_ctx))
+            return hipErrorInvalidValue;
         S.W[i] = to_wv(M[i]);
         S.out[i] = out[i];
         wgs += (M[i].L.rows + kPfRows - 1) / kPfRows * ((ntok + kPfTokWg - 1) / kPfTokWg);
@@ -968,16 +960,7 @@ hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, uint32_t nseg
 }
 
 hipError_t pi_pf_gemm(const pi_pf_mat &M, pi_pf_q8 a, uint32_t ntok, float *out, bool resid, hipStream_t s) {
-    return pi_pf_gemm_multi(&M, &out, 1, a, ntok, resid, s);
-}
-
-hipError_t pi_pf_rope_kv(float *Q, const float *K, const float *V, const float *cos_tab, const float *sin_tab,
-                         uint32_t pos0, uint32_t ntok, uint32_t n_head, uint32_t n_kv, uint32_t half, float *kc,
-                         float *vc, uint32_t n_ctx, hipStream_t s) {
-    if (ntok == 0 || ntok > PI_PF_MAX_TOK || pos0 + ntok > n_ctx || half > 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_rope_kv, dim3(ntok), dim3(256), 0, s, Q, K, V, cos_tab, sin_tab, pos0, n_head, n_kv, half,
-                       kc, vc, n_ctx);
-    return hipGetLastError();
+    return pi_pf_gemm_multi(&M, &out, nullptr, 1, a, ntok, resid, nullptr, s);
 }
 
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
