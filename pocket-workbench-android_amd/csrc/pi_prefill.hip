@@ -480,7 +480,7 @@ __global__ __launch_bounds__(256) void k_pf_embed(const uint8_t *__restrict__ E,
 // ahead); thread 0 adds the squares in order; pairs of lanes then quantize
 // half a block each.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kNormPad = 64;
+constexpr uint32_t kNormPad = 128;   // floats the chain reads past the row (2 x 16 float4)
 
 __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X, const float *__restrict__ w,
                                                     uint32_t ne, float eps, pi_pf_q8 o) {
@@ -499,7 +499,7 @@ __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X,
     if (tid == 0) {
         // ss += v * v in order (model.rs:812-822): the products are formed above
         float ss = 0.0f;
-        lds_chain4<8>(reinterpret_cast<const float4 *>(sq), ne / 4, [&](const float4 &q) {
+        lds_chain4<16>(reinterpret_cast<const float4 *>(sq), ne / 4, [&](const float4 &q) {
             ss += q.x;
             ss += q.y;
             ss += q.z;
@@ -531,32 +531,46 @@ __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X,
 }
 
 // ---------------------------------------------------------------------------
-// h = silu(gate) * up, then Q8 of h: a lane per half block, a pair per block.
+// h = silu(gate) * up, then Q8 of h: a lane per 4 elements, 8 consecutive
+// lanes per 32-element block (the block's maximum and quant sum reduced over
+// the 8 lanes with DPP; both are exact in any order).
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ G, const float *__restrict__ U,
                                                       uint32_t n_ff, pi_pf_q8 o) {
-    const uint32_t t = blockIdx.x, nb = n_ff / 32;
-    const uint32_t p = blockIdx.y * blockDim.x + threadIdx.x;
-    if (p >= 2 * nb) return;   // 2 * nb is even: pairs stay together
-    const uint32_t b = p >> 1, hh = p & 1u;
-    const float4 *g4 = reinterpret_cast<const float4 *>(G + (uint64_t)t * n_ff + 16 * p);
-    const float4 *u4 = reinterpret_cast<const float4 *>(U + (uint64_t)t * n_ff + 16 * p);
-    float v[16];
+    const uint32_t t = blockIdx.x, nq = n_ff / 4;
+    const uint32_t q = blockIdx.y * blockDim.x + threadIdx.x;
+    if (q >= nq) return;   // nq is a multiple of 8 and so is every workgroup: blocks stay whole
+    const float4 gg = reinterpret_cast<const float4 *>(G + (uint64_t)t * n_ff)[q];
+    const float4 uu = reinterpret_cast<const float4 *>(U + (uint64_t)t * n_ff)[q];
+    const float ga[4] = {gg.x, gg.y, gg.z, gg.w}, ua[4] = {uu.x, uu.y, uu.z, uu.w};
+    float v[4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float4 gg = g4[j], uu = u4[j];
-        const float ga[4] = {gg.x, gg.y, gg.z, gg.w}, ua[4] = {uu.x, uu.y, uu.z, uu.w};
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float sg = ga[e] / (1.0f + pi_expf(-ga[e]));
-            v[4 * j + e] = sg * ua[e];
-        }
+    for (int e = 0; e < 4; e++) {
+        const float sg = ga[e] / (1.0f + pi_expf(-ga[e]));
+        v[e] = sg * ua[e];
     }
-    uint32_t w4[4];
-    float dd;
-    int sum;
-    q8_pair_core(v, w4, dd, sum);
-    pf_store_pair(o, t, b, hh, w4, dd, sum);
+    // Q8 of the block (quant_int.rs:33-55): amax ignores NaN, d = amax / 127,
+    // inv = 1 / d, roundf half away from zero, clamped
+    float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    amax = fmaxf(amax, dpp<kDppXor1>(amax));
+    amax = fmaxf(amax, dpp<kDppXor2>(amax));
+    amax = fmaxf(amax, dpp<kDppHalfMirror>(amax));
+    amax = fmaxf(amax, 0.0f);   // all-NaN block: 0
+    const float dd = amax / 127.0f;
+    const float inv = dd > 0.0f ? 1.0f / dd : 0.0f;
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) word |= ((uint32_t)q8_round_clamp(v[e] * inv) & 0xFFu) << (8 * e);
+    int sum = sdot4((int)word, 0x01010101, 0);
+    sum += dpp<kDppXor1>(sum);
+    sum += dpp<kDppXor2>(sum);
+    sum += dpp<kDppHalfMirror>(sum);
+    const uint32_t b = q / 8, k = q % 8;   // block, quad within the block
+    *reinterpret_cast<uint32_t *>(o.q + pfq_off(b, k / 2, t) + 4 * (k & 1u)) = word;
+    if (k == 0) {
+        o.d[b * PI_PF_MAX_TOK + t] = dd;
+        o.s[b * PI_PF_MAX_TOK + t] = sum;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -974,6 +988,6 @@ hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t
 
 hipError_t pi_pf_swiglu_q8(const float *G, const float *U, uint32_t ntok, uint32_t n_ff, pi_pf_q8 o, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || n_ff % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_swiglu_q8, dim3(ntok, (n_ff / 16 + 255) / 256), dim3(256), 0, s, G, U, n_ff, o);
+    hipLaunchKernelGGL(k_pf_swiglu_q8, dim3(ntok, (n_ff / 4 + 255) / 256), dim3(256), 0, s, G, U, n_ff, o);
     return hipGetLastError();
 }
