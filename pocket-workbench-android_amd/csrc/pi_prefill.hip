@@ -721,8 +721,10 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
 
     // ---- pass 1: scores and maxima -----------------------------------------
     float mx[TPW];
+    // scores of this lane's positions in steps 0 and 1, kept for pass 2
+    float sA[TPW], sB[TPW];
 #pragma unroll
-    for (uint32_t j = 0; j < TPW; j++) mx[j] = -INFINITY;
+    for (uint32_t j = 0; j < TPW; j++) mx[j] = sA[j] = sB[j] = -INFINITY;
     stream(std::false_type{}, [&](uint32_t c, const float *cur, auto) {
         const uint32_t p = c * kAttStep + lane;
         if (nv && p <= pos_last) {
@@ -748,6 +750,8 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                     const float sv = sc[j] * scale;
                     srow(j)[p] = sv;
                     mx[j] = fmaxf(mx[j], sv);
+                    if (c == 0) sA[j] = sv;
+                    if (c == 1) sB[j] = sv;
                 }
             }
         }
@@ -762,17 +766,6 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
 #pragma unroll
     for (uint32_t j = 0; j < TPW; j++) acc[j] = 0.0f;
     const uint32_t st_t = tg * TW + lane;   // wavefront 4: lane = token
-    // scores of steps 0 and 1 (this lane's position, clamped to written ones)
-    float sA[TPW], sB[TPW];
-#pragma unroll
-    for (uint32_t j = 0; j < TPW; j++) {
-        sA[j] = sB[j] = 0.0f;
-        if (j < nv) {
-            const uint32_t pj = pos0 + t0 + j;
-            sA[j] = srow(j)[min(lane, pj)];
-            sB[j] = srow(j)[min(kAttStep + lane, pj)];
-        }
-    }
     auto add_sums = [&](uint32_t c, uint32_t par) {   // wavefront 4: the e of step c
         const uint32_t p0 = c * kAttStep;
         if (lane < TW && st_t < ntok && pos0 + st_t >= p0) {
