@@ -277,6 +277,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=2, help="untimed full decodes first")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graphs", action="store_true", help="launch kernels one by one (for profilers)")
+    ap.add_argument("--per-stage", action="store_true",
+                    help="engine tokens on the per-stage kernels, no cooperative launch (for profilers)")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill and long-context sections")
     ap.add_argument("--profile-gemv", action="store_true", help="GEMV launches and a device copy only")
     ap.add_argument("--profile-decode", action="store_true", help="one 32-token decode and a device copy only")
@@ -301,6 +303,8 @@ def main():
 
 def run(args, skip, steps, warmup, b, t_start):
     b.use_graphs(not args.no_graphs)
+    if args.per_stage:
+        b.use_persistent(False)
     log(f"device: {b.name()}")
     if args.profile_gemv:
         profile_gemv(b)
