@@ -145,7 +145,7 @@ def bench_prefill(b, model, spec):
     _, sa = eng.generate(ids[:2048], 1)
     _, sb = eng.generate(ids, 1)
     return {"prompt_tokens": 2048, "prefill_ms": round(sa["prefill_ms"], 2),
-            "tok_s": round(2048 / (sa["prefill_ms"] / 1000.0), 1), "chunk_tokens": 32, "pass_tokens": 256,
+            "tok_s": round(2048 / (sa["prefill_ms"] / 1000.0), 1), "chunk_tokens": 32, "pass_tokens": b.prefill_pass_tokens(),
             "extension": {"new_tokens": sb["prefill_tokens"], "reused_tokens": sb["prefill_cached_tokens"],
                           "prefill_ms": round(sb["prefill_ms"], 2),
                           "tok_s": round(sb["prefill_tokens"] / (sb["prefill_ms"] / 1000.0), 1)}}

@@ -267,10 +267,15 @@ int  pi_hip_use_graphs(pi_ctx *ctx, int enable);
 int  pi_hip_use_persistent(pi_ctx *ctx, int enable);
 /* Prompt chunks of 2..32 tokens (and engine forwards of several consecutive
  * tokens) run on the batched int8-MFMA prefill kernels by default, in passes
- * of up to 256 tokens that may span several chunks; enable = 0 evaluates them
- * one token at a time.  Results are identical either way (the reference's
- * multi-token float orders, model.rs:812-822, 1028-1038). */
+ * that may span several chunks; enable = 0 evaluates them one token at a
+ * time.  Results are identical either way (the reference's multi-token float
+ * orders, model.rs:812-822, 1028-1038). */
 int  pi_hip_use_batch_prefill(pi_ctx *ctx, int enable);
+/* Tokens per batched prefill pass of the bound model: 1024, halved while the
+ * pass's attention scores (pass * n_head * n_ctx floats) exceed 1 GiB; 0 when
+ * no model is bound or it is outside the batched kernels' limits.  No
+ * counterpart in the reference, whose passes are its 32-token chunks. */
+int  pi_hip_prefill_pass_tokens(const pi_ctx *ctx);
 /* 1 when the bound model runs on the persistent kernel, 0 otherwise. */
 int  pi_hip_persistent_active(const pi_ctx *ctx);
 /* Stage tracing of the persistent kernel (the reference's GenStats wall

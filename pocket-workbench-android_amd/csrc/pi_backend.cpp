@@ -117,6 +117,7 @@ struct Engine {
     size_t mega_lds = 0;
     // batched prefill (pi_prefill.hip): token-major chunk buffers
     bool pf_ok = false;
+    uint32_t pf_pass = 0;   // tokens per device pass (a multiple of 64, at most PI_PF_MAX_TOK)
     float *pfX = nullptr, *pfQ = nullptr, *pfG = nullptr, *pfU = nullptr;
     float *pfS = nullptr;   // attention scores of a pass: [token][head][n_ctx]
     int8_t *pfq = nullptr;
@@ -610,14 +611,22 @@ int build_prefill(pi_ctx *c, Engine &e) {
     e.pf_ok = false;
     const uint32_t qdim = e.n_head * e.dh;
     if (e.dh != 64 || e.n_embd / 32 > 256 || e.n_rot / 2 > 32) return PI_OK;
-    const uint64_t T = PI_PF_MAX_TOK;
+    // Larger passes fill the machine better (the attention's workgroups come in
+    // whole rounds, the weights stream once per pass); the attention scores of
+    // a pass, pass * n_head * n_ctx floats, bound it at long context.
+    const uint64_t srow = e.n_head * pi_pf_score_stride(e.n_ctx) * 4;
+    uint32_t pass = PI_PF_MAX_TOK;
+    while (pass > 64 && pass * srow > PI_PF_SCORE_BUDGET) pass /= 2;
+    const uint64_t T = pass, TQ = PI_PF_MAX_TOK;   // Q8 activations keep the PI_PF_MAX_TOK stride
     const uint64_t kmax = std::max(std::max(e.n_embd, e.n_ff), qdim);
     int r;
     if ((r = dalloc(c, &e.pfX, T * e.n_embd)) || (r = dalloc(c, &e.pfQ, T * qdim)) ||
         (r = dalloc(c, &e.pfG, T * e.n_ff)) || (r = dalloc(c, &e.pfU, T * e.n_ff)) ||
-        (r = dalloc(c, &e.pfq, T * kmax)) || (r = dalloc(c, &e.pfd, T * kmax / 32)) || (r = dalloc(c, &e.pfs, T * kmax / 32)) ||
-        (r = dalloc(c, &e.pfS, T * e.n_head * pi_pf_score_stride(e.n_ctx))) || (r = dalloc(c, &e.pf_ids, 2 * T)))
+        (r = dalloc(c, &e.pfq, TQ * kmax)) || (r = dalloc(c, &e.pfd, TQ * kmax / 32)) ||
+        (r = dalloc(c, &e.pfs, TQ * kmax / 32)) || (r = dalloc(c, &e.pfS, T * e.n_head * pi_pf_score_stride(e.n_ctx))) ||
+        (r = dalloc(c, &e.pf_ids, 2 * T)))
         return r;
+    e.pf_pass = pass;
     e.pf_ok = true;
     return PI_OK;
 }
@@ -626,7 +635,7 @@ bool use_pf(const pi_ctx *c, const Engine &e) { return c->use_batch_prefill && e
 
 pi_pf_mat pfmat(const pi_tensor *t) { return pi_pf_mat{t->dev, t->L}; }
 
-// One pass of ntok (1..PI_PF_MAX_TOK) consecutive tokens at positions pos0..
+// One pass of ntok (1..pf_pass) consecutive tokens at positions pos0..
 // through every layer on the batched prefill kernels; the residual stream
 // ends in pfX.
 hipError_t pf_chunk(const pi_ctx *c, const Engine &e, const uint32_t *ids_dev, uint32_t pos0, uint32_t ntok) {
@@ -858,6 +867,8 @@ int pi_hip_use_batch_prefill(pi_ctx *c, int enable) {
 }
 
 int pi_hip_persistent_active(const pi_ctx *c) { return c && c->eng && use_mega(c, *c->eng) ? 1 : 0; }
+
+int pi_hip_prefill_pass_tokens(const pi_ctx *c) { return c && c->eng && c->eng->pf_ok ? (int)c->eng->pf_pass : 0; }
 
 int pi_hip_stage_trace(pi_ctx *c, int enable) {
     if (!c) return PI_E_INVALID;
@@ -1318,15 +1329,15 @@ static int forward_impl(pi_ctx *c, const uint32_t *ids, const int32_t *pos, int 
     for (int i = 1; i < b; i++) consecutive &= pos[i] == pos[0] + i;
     if (b > 1 && consecutive && use_pf(c, *e)) {
         // a batch of more than one token: every token in the multi-token
-        // orders, in passes of at most PI_PF_MAX_TOK on the batched kernels
+        // orders, in passes of at most pf_pass tokens on the batched kernels
         if (want_logits) {
             int r = set_state(c, *e, pos[b - 1], ids[b - 1], 0, 0);
             if (r) return r;
         }
         uint32_t last_nt = 0;
-        for (int off = 0; off < b; off += (int)PI_PF_MAX_TOK) {
+        for (int off = 0; off < b; off += (int)e->pf_pass) {
             if (cancellable && c->stop.load()) return fail(c, PI_E_STOPPED, "generation stopped");
-            const uint32_t nt = std::min<uint32_t>(PI_PF_MAX_TOK, (uint32_t)(b - off));
+            const uint32_t nt = std::min<uint32_t>(e->pf_pass, (uint32_t)(b - off));
             HIPC(c, hipMemcpyAsync(e->pf_ids, ids + off, nt * 4, hipMemcpyHostToDevice, c->stream));
             HIPC(c, pf_chunk(c, *e, e->pf_ids, (uint32_t)pos[off], nt));
             last_nt = nt;
@@ -1520,13 +1531,13 @@ int pi_hip_generate(pi_ctx *c, const uint32_t *prompt, size_t n, const pi_genopt
     if (use_pf(c, *e)) {
         // Reference chunks of 32 from `reused`: every token of a chunk of more
         // than one token runs on the batched prefill kernels, in passes of up
-        // to PI_PF_MAX_TOK tokens that may span several chunks; a chunk of one
+        // to pf_pass tokens that may span several chunks; a chunk of one
         // (only the last can be) runs in the batch-1 order.  The last pass
         // also computes the logits and the first greedy id of its last token.
         const size_t batched_end = last_chunk == 1 ? n - 1 : n;
         while (off < n) {
             if (c->stop.load()) { stopped = true; break; }
-            const size_t end = off < batched_end ? std::min(batched_end, off + PI_PF_MAX_TOK) : n;
+            const size_t end = off < batched_end ? std::min<size_t>(batched_end, off + e->pf_pass) : n;
             const bool last = end == n;
             if (off >= batched_end) {
                 if (mega) {

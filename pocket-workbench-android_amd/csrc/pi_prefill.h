@@ -11,7 +11,10 @@
 
 #include "pi_common.h"
 
-constexpr uint32_t PI_PF_MAX_TOK = 256;
+constexpr uint32_t PI_PF_MAX_TOK = 1024;
+// Score scratch a pass may use (pi_pf_attn): the engine halves its pass size
+// from PI_PF_MAX_TOK until the pass's scores fit.
+constexpr uint64_t PI_PF_SCORE_BUDGET = 1ull << 30;
 
 // A weight matrix in the tiled layout (pi_common.h), as the prefill GEMM reads it.
 struct pi_pf_mat {
@@ -57,7 +60,7 @@ hipError_t pi_pf_gemm_multi(const pi_pf_mat *M, float *const *out, const uint32_
                             uint32_t ntok, bool resid, const pi_pf_rope *rope, hipStream_t s);
 // Attention of every token over positions 0..its own (model.rs:993-1087,
 // multi-token orders), then Q8 of the output.  scores: scratch of
-// PI_PF_MAX_TOK * n_head * pi_pf_score_stride(n_ctx) floats.
+// ntok * n_head * pi_pf_score_stride(n_ctx) floats.
 constexpr uint64_t pi_pf_score_stride(uint32_t n_ctx) { return ((uint64_t)n_ctx + 31) & ~31ull; }
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
                       uint32_t n_kv, uint32_t n_ctx, float scale, float *scores, pi_pf_q8 out, hipStream_t s);

@@ -49,7 +49,7 @@ EXPORTS = [
     "pi_hip_kv_write", "pi_hip_kv_read", "pi_hip_kv_fill_normal", "pi_hip_kv_set_tokens",
     "pi_hip_request_stop", "pi_hip_clear_stop", "pi_hip_use_graphs", "pi_hip_last_decode_us",
     "pi_hip_time_kernels", "pi_hip_last_kernel_us", "pi_hip_time_gemv_x",
-    "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
+    "pi_hip_use_persistent", "pi_hip_persistent_active", "pi_hip_use_batch_prefill", "pi_hip_prefill_pass_tokens", "pi_hip_stage_trace", "pi_hip_stage_trace_read",
     "pi_synth_q4k_random", "pi_synth_q6k_random", "pi_synth_normal", "pi_synth_tensor", "pi_synth_kv_normal",
     "pi_quantize_row", "pi_rng_new", "pi_rng_next_u64", "pi_sample",
     "pi_gguf_open", "pi_gguf_parse", "pi_gguf_close", "pi_gguf_version", "pi_gguf_data_offset", "pi_gguf_n_kv",
@@ -148,6 +148,7 @@ def load_library(path: Path | str | None = None) -> C.CDLL:
         "pi_hip_use_graphs": (i32, [vp, i32]),
         "pi_hip_use_persistent": (i32, [vp, i32]),
         "pi_hip_persistent_active": (i32, [vp]),
+        "pi_hip_prefill_pass_tokens": (i32, [vp]),
         "pi_hip_use_batch_prefill": (i32, [vp, i32]),
         "pi_hip_stage_trace": (i32, [vp, i32]),
         "pi_hip_stage_trace_read": (i32, [vp, vp, C.c_size_t, C.POINTER(C.c_uint32), C.POINTER(C.c_uint32)]),
@@ -446,6 +447,10 @@ class HipBackend:
 
     def persistent_active(self) -> bool:
         return self.lib.pi_hip_persistent_active(self.ctx) == 1
+
+    def prefill_pass_tokens(self) -> int:
+        """Tokens per batched prefill pass of the bound model (0: none)."""
+        return self.lib.pi_hip_prefill_pass_tokens(self.ctx)
 
     def stage_trace(self, enable: bool) -> None:
         self.check(self.lib.pi_hip_stage_trace(self.ctx, int(enable)))

@@ -113,19 +113,40 @@ def test_tiny_generate_matches_oracle(pih, backend, oracle, tiny, n_prompt):
     assert _bits_equal(eng.logits(), ref.logits())
 
 
-@pytest.mark.parametrize("n_prompt", [300, 289, 257])
+@pytest.mark.parametrize("n_prompt", [1100, 1057, 1025])
 def test_tiny_generate_passes_span_chunks(pih, backend, oracle, tiny, n_prompt):
-    """Prompts longer than one 256-token device pass: the passes group the
-    reference's 32-token chunks (300: passes of 256 + 44; 289: 256 + 32, then
-    the single-token last chunk; 257: 256, then the single token); ids and
-    final logits equal the oracle's."""
-    eng = pih.HipEngine(backend, tiny, n_ctx=512)
-    ref = oracle.OracleEngine(tiny, n_ctx=512, threads=4)
+    """Prompts longer than one 1024-token device pass: the passes group the
+    reference's 32-token chunks (1100: passes of 1024 + 76; 1057: 1024 + 32,
+    then the single-token last chunk; 1025: 1024, then the single token); ids
+    and final logits equal the oracle's."""
+    eng = pih.HipEngine(backend, tiny, n_ctx=1200)
+    assert backend.prefill_pass_tokens() == 1024
+    ref = oracle.OracleEngine(tiny, n_ctx=1200, threads=4)
     prompt = [(i * 29 + 3) % 1000 for i in range(n_prompt)]
     got, st = eng.generate(prompt, 8)
     want, _ = ref.generate(prompt, 8)
     assert got == want and st["prefill_tokens"] == n_prompt
     assert _bits_equal(eng.logits(), ref.logits())
+
+
+_WIDE_REF = {}
+
+
+def test_pass_shrinks_at_long_context(pih, backend, oracle):
+    """With 36 heads at n_ctx 8192 a 1024-token pass would need 1.2 GB of
+    attention scores (1024 x 36 x 8192 floats), over the 1 GiB budget: the
+    pass halves to 512, and a 540-token prompt (passes of 512 + 28) still
+    equals the oracle."""
+    model = pih.synth_model(pih.tiny_spec(n_layer=2, n_embd=2304, n_ff=512, n_head=36, n_vocab=1000), seed=29)
+    eng = pih.HipEngine(backend, model, n_ctx=8192)
+    assert backend.prefill_pass_tokens() == 512
+    prompt = [(i * 31 + 7) % 1000 for i in range(540)]
+    got, _ = eng.generate(prompt, 2)
+    if not _WIDE_REF:   # the oracle's result does not depend on the engine mode
+        ref = oracle.OracleEngine(model, n_ctx=8192, threads=8)
+        _WIDE_REF["ids"], _ = ref.generate(prompt, 2)
+        _WIDE_REF["logits"] = ref.logits().copy()
+    assert got == _WIDE_REF["ids"] and _bits_equal(eng.logits(), _WIDE_REF["logits"])
 
 
 def test_tiny_attention_skips_zero_weights(pih, backend, oracle, tiny):
