@@ -603,6 +603,11 @@ constexpr uint32_t kAttBuf = kAttStep * kKRow;  // floats per staging buffer (>=
 static_assert(kAttBuf >= 64 * kVRow, "staging buffer holds a transposed V step");
 static_assert(kAttTok <= 64, "wavefront 4 holds one token per lane");
 
+// Parts per head in the attention's XCD assignment: 8 / gcd(n_head, 8).
+__host__ __device__ constexpr uint32_t pf_att_parts(uint32_t n_head) {
+    return (n_head % 8 == 0) ? 1u : (n_head % 4 == 0 ? 2u : (n_head % 2 == 0 ? 4u : 8u));
+}
+
 template <uint32_t TPW>
 __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
                                                          const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
@@ -616,11 +621,19 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
     float *eb = qs + TW * DH;                   // [2][TW][64]: e of a step per token, two steps alternating
     float *misc = eb + 2 * TW * kAttStep;       // per-token sums
     uint32_t *vbad = reinterpret_cast<uint32_t *>(misc + TW);   // [2][4]: a staging wavefront saw a non-finite V
-    // Workgroup b runs on XCD b % 8 (round-robin dispatch): every workgroup of
-    // head h gets b % 8 == h % 8, so a head's K/V rows are read into one L2.
-    const uint32_t ntg = (ntok + TW - 1) / TW, xcd = blockIdx.x & 7u, rest = blockIdx.x >> 3;
-    const uint32_t tg = rest % ntg, h = (rest / ntg) * 8 + xcd;
-    if (h >= n_head) return;   // before any barrier: the whole workgroup leaves
+    // Workgroup b runs on XCD b % 8 (round-robin dispatch).  The token groups
+    // of a head are split into P interleaved parts (tg % P), P = 8 / gcd(n_head,
+    // 8), so the n_head * P units (head, part) divide evenly over the 8 XCDs:
+    // unit u goes to XCD u % 8, and a head's K/V rows are read into P L2s.
+    // Within an XCD the units advance together, the last token groups (the
+    // most positions) first, so the workgroups that start last are the short
+    // ones.
+    const uint32_t ntg = (ntok + TW - 1) / TW, xcd = blockIdx.x & 7u, r = blockIdx.x >> 3;
+    const uint32_t P = pf_att_parts(n_head), nu = (n_head * P - xcd + 7) / 8;   // units of this XCD
+    const uint32_t u = xcd + 8 * (r % nu), level = r / nu, part = u % P, h = u / P;
+    const uint32_t cnt = (ntg - part + P - 1) / P;   // token groups part, part + P, ... below ntg
+    if (level >= cnt) return;   // before any barrier: the whole workgroup leaves
+    const uint32_t tg = part + P * (cnt - 1 - level);
     const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
     const bool stager = w < 4;
     const uint32_t t0 = tg * TW + (w & 3u) * TPW;   // first token of this wavefront
@@ -973,7 +986,8 @@ hipError_t pi_pf_gemm(const pi_pf_mat &M, pi_pf_q8 a, uint32_t ntok, float *out,
 hipError_t pi_pf_attn(const float *Q, const float *kc, const float *vc, uint32_t pos0, uint32_t ntok, uint32_t n_head,
                       uint32_t n_kv, uint32_t n_ctx, float scale, float *scores, pi_pf_q8 o, hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || pos0 + ntok > n_ctx || n_kv == 0 || n_head % n_kv) return hipErrorInvalidValue;
-    const uint32_t blocks = 8 * ((ntok + kAttTok - 1) / kAttTok) * ((n_head + 7) / 8);
+    const uint32_t P = pf_att_parts(n_head), ntg = (ntok + kAttTok - 1) / kAttTok;
+    const uint32_t blocks = 8 * ((n_head * P + 7) / 8) * ((ntg + P - 1) / P);   // XCD 0 has the most units
     hipLaunchKernelGGL(k_pf_attn<kAttTpw>, dim3(blocks), dim3(kAttThreads), 0, s, Q, kc, vc, pos0, ntok, n_head, n_head / n_kv,
                        n_ctx, scale, scores, o.q, o.d, o.s);
     return hipGetLastError();
