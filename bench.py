@@ -327,7 +327,7 @@ def run(args, skip, steps, warmup, b, t_start):
               "bytes_per_launch": q5_bytes, "us": round(u5, 2),
               "achieved_gbs": round(q5_bytes / (u5 * 1e-6) / 1e9, 1),
               "frac": round(q5_bytes / (u5 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-              "bound": "one dependent add per element per lane (latency), not HBM"}
+              "bound": "the row's dependent adds in element order (one chain lane per row; ~7.5 cycles per add), not HBM"}
         log(f"gemv q5_k (f32 path): {g5}")
         log(f"gemv q4k: {g4}")
         log(f"gemv q6k: {g6}")

@@ -124,8 +124,9 @@ size_t pi_hip_tensor_bytes(const pi_tensor *t);
  * blocks in its LDS (quant_int.rs:17-56), then runs the fused dequant +
  * int8-dot GEMV (quant_int.rs:330-419).  (Rows too long for LDS take a Q8
  * pre-pass into context staging memory instead; same results.)  f32-path
- * types: one lane per row adds its dequantized weights times x in element
- * order (quant.rs:377-441). */
+ * types: each row's dequantized weights times x are added in element order
+ * (quant.rs:377-441) by one lane per row while other wavefronts form the
+ * products. */
 int  pi_hip_gemv_dev(pi_ctx *ctx, const pi_tensor *w, const float *x_dev, float *y_dev);
 /* Same GEMV on already-quantized activations (device pointers, lane 0);
  * int8-path types only (PI_E_UNSUPPORTED otherwise). */

@@ -1,5 +1,6 @@
 // Single-token f32 dot of the GGUF types without an int8 path (quant.rs:
-// 377-441): one lane per row, weights in their GGUF row layout.
+// 377-441): one add chain per row, products formed by other wavefronts,
+// weights in their GGUF row layout.
 #pragma once
 
 #include <hip/hip_runtime.h>
