@@ -819,18 +819,18 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
                 const float4 *src = wlane ? reinterpret_cast<const float4 *>(L.sc + (c - 1) * kChunk)
                                           : reinterpret_cast<const float4 *>(L.hb + ((c - 1) & 1u) * DHH * kChunkPad +
                                                                              lane * kChunkPad);
+                // all 16 reads of the chunk first (the scheduling barrier keeps
+                // them ahead of the adds), one LDS latency per step
+                float4 t[16];
 #pragma unroll
-                for (int h2 = 0; h2 < 2; h2++) {
-                    float4 t[8];
+                for (int q = 0; q < 16; q++) t[q] = src[q ^ hr];
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int q = 0; q < 8; q++) t[q] = src[(8 * h2 + q) ^ hr];
-#pragma unroll
-                    for (int q = 0; q < 8; q++) {
-                        acc = acc + t[q].x;
-                        acc = acc + t[q].y;
-                        acc = acc + t[q].z;
-                        acc = acc + t[q].w;
-                    }
+                for (int q = 0; q < 16; q++) {
+                    acc = acc + t[q].x;
+                    acc = acc + t[q].y;
+                    acc = acc + t[q].z;
+                    acc = acc + t[q].w;
                 }
             }
             lds_barrier();
