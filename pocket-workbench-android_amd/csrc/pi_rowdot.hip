@@ -34,8 +34,8 @@ __device__ __forceinline__ float h2f_bits(uint32_t bits) {
     return (float)h;
 }
 
-// Block bytes in registers: n 32-bit words (4-aligned blocks) or n/2 of them
-// assembled from 16-bit loads (blocks of 22 and 110 bytes are 2-aligned).
+// A whole 32-element block in registers: 32-bit words (4-aligned blocks), or
+// words assembled from 16-bit loads (Q5_0's 22-byte blocks are 2-aligned).
 template <uint32_t BB>
 struct Blk {
     static constexpr uint32_t NW = (BB + 3) / 4;
