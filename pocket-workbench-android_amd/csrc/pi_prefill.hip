@@ -577,9 +577,11 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ 
 // Attention: a workgroup serves 4 * TPW consecutive tokens of one head with 5
 // wavefronts; wavefront w (0-3) serves tokens TPW*w..TPW*w+TPW-1 of them.
 // K, then V, rows are staged through two LDS buffers 64 positions per step
-// by wavefronts 0-3, each step's rows loaded into registers two steps ahead
+// by wavefronts 0-3, each step's rows loaded into registers one step ahead
 // (one barrier per step); every staged row feeds the chains of all the
-// workgroup's tokens.
+// workgroup's tokens.  96 registers per lane and 40 KB of LDS per workgroup
+// keep five wavefronts per SIMD (four workgroups per CU), whose steps hide
+// each other's load latency better than a second step in flight would.
 // Pass 1, scores (model.rs:1028-1038, scalar dot in d order, * scale): lane
 // = position, one chain per token of the wavefront; each score goes to the
 // token's row of a score scratch in global memory, and the maximum is kept.
@@ -609,18 +611,22 @@ __host__ __device__ constexpr uint32_t pf_att_parts(uint32_t n_head) {
 }
 
 template <uint32_t TPW>
-__global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
+__global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))) void k_pf_attn(const float *__restrict__ Q, const float *__restrict__ kc,
                                                          const float *__restrict__ vc, uint32_t pos0, uint32_t ntok,
                                                          uint32_t n_head, uint32_t group, uint32_t n_ctx, float scale,
                                                          float *__restrict__ scr, int8_t *__restrict__ oq,
                                                          float *__restrict__ od, int32_t *__restrict__ os) {
     constexpr uint32_t DH = 64, TW = 4 * TPW;
-    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep + TW + 8];
+    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep];
     float *const buf0 = lds, *const buf1 = lds + kAttBuf;
     float *qs = lds + 2 * kAttBuf;              // [TW][64]
     float *eb = qs + TW * DH;                   // [2][TW][64]: e of a step per token, two steps alternating
-    float *misc = eb + 2 * TW * kAttStep;       // per-token sums
-    uint32_t *vbad = reinterpret_cast<uint32_t *>(misc + TW);   // [2][4]: a staging wavefront saw a non-finite V
+    // per-token sums and the non-finite-V flags live in the staging rows'
+    // padding (column 64 of buf0's rows 0..7 and 8..8+TW), which no step reads
+    // or writes
+    static_assert(kKRow == kVRow && kKRow > 64 && 8 + TW <= kAttStep, "flags and sums fit the row padding");
+    auto misc_at = [&](uint32_t i) -> float & { return buf0[(8u + i) * kKRow + 64u]; };
+    auto vbad_at = [&](uint32_t i) -> uint32_t & { return reinterpret_cast<uint32_t *>(buf0)[i * kKRow + 64u]; };
     // Workgroup b runs on XCD b % 8 (round-robin dispatch).  The token groups
     // of a head are split into P interleaved parts (tg % P), P = 8 / gcd(n_head,
     // 8), so the n_head * P units (head, part) divide evenly over the 8 XCDs:
@@ -701,10 +707,10 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
             fin = fin && __builtin_isfinite(R.v[j].x) && __builtin_isfinite(R.v[j].y) &&
                   __builtin_isfinite(R.v[j].z) && __builtin_isfinite(R.v[j].w);
         const bool bad = __ballot(!fin) != 0;
-        if (lane == 0) vbad[(bf == buf1 ? 4u : 0u) + w] = bad ? 1u : 0u;
+        if (lane == 0) vbad_at((bf == buf1 ? 4u : 0u) + w) = bad ? 1u : 0u;
     };
-    // Runs body(c, buffer of step c, parity of c) for every step; rows of step
-    // c + 1 are stored while step c is used, rows of step c + 2 are in flight.
+    // Runs body(c, buffer of step c, parity of c) for every step; the rows of
+    // step c + 1 are in flight while step c is used and stored after it.
     auto stream = [&](auto transposed, auto &&body) {
         auto load = [&](uint32_t c) {
             if constexpr (decltype(transposed)::value) return load_v(c);
@@ -715,20 +721,19 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
             else store_k(R, bf);
         };
         Rows A = load(0);
-        Rows B = load(min(1u, nsteps - 1));
         put(A, buf0);
         __syncthreads();
-        A = load(min(2u, nsteps - 1));
+        A = load(min(1u, nsteps - 1));
         for (uint32_t c = 0; c < nsteps; c += 2) {
             body(c, buf0, std::integral_constant<uint32_t, 0>{});
-            if (c + 1 < nsteps) put(B, buf1);
+            if (c + 1 < nsteps) put(A, buf1);
             __syncthreads();
             if (c + 1 >= nsteps) break;
-            B = load(min(c + 3, nsteps - 1));
+            A = load(min(c + 2, nsteps - 1));
             body(c + 1, buf1, std::integral_constant<uint32_t, 1>{});
             if (c + 2 < nsteps) put(A, buf0);
             __syncthreads();
-            A = load(min(c + 4, nsteps - 1));
+            A = load(min(c + 3, nsteps - 1));
         }
     };
 
@@ -820,8 +825,8 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
                 if (par) sB[j] = sn;
                 else sA[j] = sn;
             }
-            const uint32_t *vb = vbad + par * 4u;
-            const bool skip = zero && (vb[0] | vb[1] | vb[2] | vb[3]) != 0u;
+            const bool skip = zero && (vbad_at(par * 4u) | vbad_at(par * 4u + 1u) | vbad_at(par * 4u + 2u) |
+                                       vbad_at(par * 4u + 3u)) != 0u;
             const float *vr = cur + lane * kVRow;
             if (full && !skip) {
 #pragma unroll
@@ -868,13 +873,13 @@ __global__ __launch_bounds__(kAttThreads) void k_pf_attn(const float *__restrict
     });
     if (w == 4) {
         add_sums(nsteps - 1, (nsteps - 1) & 1u);
-        if (lane < TW) misc[lane] = sum;
+        if (lane < TW) misc_at(lane) = sum;
     }
     __syncthreads();
     if (w < 4) {
 #pragma unroll
         for (uint32_t j = 0; j < TPW; j++) {
-            const float tot = misc[(w & 3u) * TPW + j];
+            const float tot = misc_at((w & 3u) * TPW + j);
             const float inv = tot > 0.0f ? 1.0f / tot : 0.0f;
             const float o = acc[j] * inv;
             const uint32_t blk = h * 2 + lane / 32, jj = lane % 32, t = t0 + j;
