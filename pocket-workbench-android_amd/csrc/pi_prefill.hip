@@ -475,58 +475,74 @@ __global__ __launch_bounds__(256) void k_pf_embed(const uint8_t *__restrict__ E,
 }
 
 // ---------------------------------------------------------------------------
-// RMSNorm (scalar order) + Q8 of one token per workgroup.  The row and its
-// squares are staged in LDS (the squares padded by floats the chain reads
-// ahead); thread 0 adds the squares in order; pairs of lanes then quantize
-// half a block each.
+// RMSNorm (scalar order) + Q8 of up to four tokens per workgroup.  The rows
+// and their squares are staged in LDS (the squares padded by floats the chain
+// reads ahead); lane 0 of wavefront j adds token j's squares in order, so the
+// tokens' add chains run on different SIMDs instead of queueing on one; pairs
+// of lanes then quantize half a block each.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kNormPad = 128;   // floats the chain reads past the row (2 x 16 float4)
+__host__ __device__ constexpr uint32_t pf_norm_region(uint32_t ne) { return 2 * ne + 2 * kNormPad; }
 
 __global__ __launch_bounds__(256) void k_pf_norm_q8(const float *__restrict__ X, const float *__restrict__ w,
-                                                    uint32_t ne, float eps, pi_pf_q8 o) {
+                                                    uint32_t ne, float eps, uint32_t ntok, uint32_t tpb, pi_pf_q8 o) {
     extern __shared__ __align__(16) float xs[];
-    __shared__ float sv;
-    const uint32_t t = blockIdx.x, tid = threadIdx.x, nb = ne / 32;
-    float *sq = xs + ne + kNormPad;   // squares, rounded as the loop rounds them
-    const float4 *x4 = reinterpret_cast<const float4 *>(X + (uint64_t)t * ne);
-    for (uint32_t i = tid; i < ne / 4; i += blockDim.x) {
-        const float4 v = x4[i];
-        reinterpret_cast<float4 *>(xs)[i] = v;
-        reinterpret_cast<float4 *>(sq)[i] = make_float4(v.x * v.x, v.y * v.y, v.z * v.z, v.w * v.w);
+    __shared__ float sv[4];
+    const uint32_t tid = threadIdx.x, nb = ne / 32, t0 = blockIdx.x * tpb, nt = min(tpb, ntok - t0);
+    const uint32_t region = pf_norm_region(ne), n4 = ne / 4;
+    // rows of tokens t0 .. t0 + nt - 1: a thread's 8 loads are issued before its stores
+    for (uint32_t base = 0; base < nt * n4; base += 256 * 8) {
+        float4 v[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t q = min(base + tid + 256 * i, nt * n4 - 1), j = q / n4;
+            v[i] = reinterpret_cast<const float4 *>(X + (uint64_t)(t0 + j) * ne)[q - j * n4];
+        }
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t q = base + tid + 256 * i, j = q / n4;
+            if (q < nt * n4) {
+                float *r = xs + j * region;
+                reinterpret_cast<float4 *>(r)[q - j * n4] = v[i];
+                reinterpret_cast<float4 *>(r + ne + kNormPad)[q - j * n4] =
+                    make_float4(v[i].x * v[i].x, v[i].y * v[i].y, v[i].z * v[i].z, v[i].w * v[i].w);
+            }
+        }
     }
-    if (tid < kNormPad) sq[ne + tid] = 0.0f;
+    for (uint32_t i = tid; i < nt * kNormPad; i += 256) xs[(i / kNormPad) * region + 2 * ne + kNormPad + i % kNormPad] = 0.0f;
     __syncthreads();
-    if (tid == 0) {
+    const uint32_t wave = tid >> 6;
+    if ((tid & 63u) == 0 && wave < nt) {
         // ss += v * v in order (model.rs:812-822): the products are formed above
         float ss = 0.0f;
-        lds_chain4<16>(reinterpret_cast<const float4 *>(sq), ne / 4, [&](const float4 &q) {
+        lds_chain4<16>(reinterpret_cast<const float4 *>(xs + wave * region + ne + kNormPad), n4, [&](const float4 &q) {
             ss += q.x;
             ss += q.y;
             ss += q.z;
             ss += q.w;
         });
-        sv = 1.0f / sqrtf(ss / (float)ne + eps);
+        sv[wave] = 1.0f / sqrtf(ss / (float)ne + eps);
     }
     __syncthreads();
-    const float sc = sv;
-    for (uint32_t p = tid; p < 2 * nb; p += blockDim.x) {   // pairs of lanes stay together
-        const uint32_t b = p >> 1, hh = p & 1u;
-        const float4 *xv = reinterpret_cast<const float4 *>(xs + 16 * p);
-        const float4 *wv = reinterpret_cast<const float4 *>(w + 16 * p);
+    for (uint32_t p = tid; p < nt * 2 * nb; p += blockDim.x) {   // pairs of lanes stay together
+        const uint32_t j = p / (2 * nb), pp = p - j * 2 * nb, b = pp >> 1, hh = pp & 1u;
+        const float sc = sv[j];
+        const float4 *xv = reinterpret_cast<const float4 *>(xs + j * region + 16 * pp);
+        const float4 *wv = reinterpret_cast<const float4 *>(w + 16 * pp);
         float v[16];
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float4 xx = xv[j], ww = wv[j];
-            v[4 * j + 0] = xx.x * sc * ww.x;
-            v[4 * j + 1] = xx.y * sc * ww.y;
-            v[4 * j + 2] = xx.z * sc * ww.z;
-            v[4 * j + 3] = xx.w * sc * ww.w;
+        for (int jj = 0; jj < 4; jj++) {
+            const float4 xx = xv[jj], ww = wv[jj];
+            v[4 * jj + 0] = xx.x * sc * ww.x;
+            v[4 * jj + 1] = xx.y * sc * ww.y;
+            v[4 * jj + 2] = xx.z * sc * ww.z;
+            v[4 * jj + 3] = xx.w * sc * ww.w;
         }
         uint32_t w4[4];
         float dd;
         int sum;
         q8_pair_core(v, w4, dd, sum);
-        pf_store_pair(o, t, b, hh, w4, dd, sum);
+        pf_store_pair(o, t0 + j, b, hh, w4, dd, sum);
     }
 }
 
@@ -924,7 +940,13 @@ hipError_t pi_pf_embed(const uint8_t *embd, uint32_t etype, uint64_t row_bytes, 
 hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps, uint32_t ntok, pi_pf_q8 o,
                          hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || ne % 32 || ne > 16384) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_pf_norm_q8, dim3(ntok), dim3(256), (2 * ne + 2 * kNormPad) * 4, s, X, w, ne, eps, o);
+    // tokens per workgroup: four while their LDS regions fit 128 KB
+    const size_t region = (size_t)pf_norm_region(ne) * 4;
+    const uint32_t tpb = region * 4 <= (128u << 10) ? 4u : (region * 2 <= (128u << 10) ? 2u : 1u);
+    const size_t lds = region * tpb;
+    hipError_t e = hipFuncSetAttribute((const void *)k_pf_norm_q8, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k_pf_norm_q8, dim3((ntok + tpb - 1) / tpb), dim3(256), lds, s, X, w, ne, eps, ntok, tpb, o);
     return hipGetLastError();
 }
 
