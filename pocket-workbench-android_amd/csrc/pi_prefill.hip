@@ -940,9 +940,13 @@ hipError_t pi_pf_embed(const uint8_t *embd, uint32_t etype, uint64_t row_bytes, 
 hipError_t pi_pf_norm_q8(const float *X, const float *w, uint32_t ne, float eps, uint32_t ntok, pi_pf_q8 o,
                          hipStream_t s) {
     if (ntok == 0 || ntok > PI_PF_MAX_TOK || ne % 32 || ne > 16384) return hipErrorInvalidValue;
-    // tokens per workgroup: four while their LDS regions fit 128 KB
+    // tokens per workgroup: one while every token can have a CU of its own,
+    // else two or four (while their LDS regions fit 128 KB), so that the chains
+    // of the tokens sharing a CU run on different SIMDs
     const size_t region = (size_t)pf_norm_region(ne) * 4;
-    const uint32_t tpb = region * 4 <= (128u << 10) ? 4u : (region * 2 <= (128u << 10) ? 2u : 1u);
+    const uint32_t want = ntok <= 256 ? 1u : (ntok <= 512 ? 2u : 4u);
+    uint32_t tpb = want;
+    while (tpb > 1 && region * tpb > (128u << 10)) tpb /= 2;
     const size_t lds = region * tpb;
     hipError_t e = hipFuncSetAttribute((const void *)k_pf_norm_q8, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
