@@ -595,17 +595,22 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ 
 // K, then V, rows are staged through two LDS buffers 64 positions per step
 // by wavefronts 0-3, each step's rows loaded into registers one step ahead
 // (one barrier per step); every staged row feeds the chains of all the
-// workgroup's tokens.  96 registers per lane and 40 KB of LDS per workgroup
-// keep five wavefronts per SIMD (four workgroups per CU), whose steps hide
-// each other's load latency better than a second step in flight would.
+// workgroup's tokens.  96 registers per lane and under 40 KB of LDS per
+// workgroup keep five wavefronts per SIMD (four workgroups per CU), whose
+// steps hide each other's load latency better than a second step in flight
+// would.
 // Pass 1, scores (model.rs:1028-1038, scalar dot in d order, * scale): lane
-// = position, one chain per token of the wavefront; each score goes to the
-// token's row of a score scratch in global memory, and the maximum is kept.
+// = position, one chain per token of the wavefront, q of the wavefront's
+// tokens in scalar registers (loaded from Q, so the LDS serves only K); each
+// score goes to the token's row of a score scratch in global memory, and the
+// maximum is kept.
 // Pass 2, per step: the wavefront reads its tokens' scores back (loaded two
-// steps ahead), forms e_p = exp(s_p - max) lane-parallel into an LDS step
-// buffer, then adds e_p * v_p[d] in position order (f32_axpy order,
-// model.rs:1056-1074: products rounded, e_p == 0 skipped), lane = dimension,
-// one chain per token, from the transposed V step; lane i of wavefront 4
+// steps ahead), forms e_p = exp(s_p - max) lane-parallel (into an LDS step
+// buffer for wavefront 4 and the partial steps; a full step reads e_p from
+// its lane into a scalar register instead), then adds e_p * v_p[d] in
+// position order (f32_axpy order, model.rs:1056-1074: products rounded,
+// e_p == 0 skipped), lane = dimension, one chain per token, from the
+// transposed V step; lane i of wavefront 4
 // adds sum += e_p of token i in position order, one step behind.  V is
 // staged as blocks of 4 positions x 4 dimensions per thread, transposed in
 // registers, so its LDS writes are 16 bytes wide and free of bank conflicts.
@@ -633,10 +638,9 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
                                                          float *__restrict__ scr, int8_t *__restrict__ oq,
                                                          float *__restrict__ od, int32_t *__restrict__ os) {
     constexpr uint32_t DH = 64, TW = 4 * TPW;
-    __shared__ __align__(16) float lds[2 * kAttBuf + TW * 64 + 2 * TW * kAttStep];
+    __shared__ __align__(16) float lds[2 * kAttBuf + 2 * TW * kAttStep];
     float *const buf0 = lds, *const buf1 = lds + kAttBuf;
-    float *qs = lds + 2 * kAttBuf;              // [TW][64]
-    float *eb = qs + TW * DH;                   // [2][TW][64]: e of a step per token, two steps alternating
+    float *eb = lds + 2 * kAttBuf;              // [2][TW][64]: e of a step per token, two steps alternating
     // per-token sums and the non-finite-V flags live in the staging rows'
     // padding (column 64 of buf0's rows 0..7 and 8..8+TW), which no step reads
     // or writes
@@ -672,12 +676,6 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
     auto srow = [&](uint32_t j) {
         return scr + ((uint64_t)min(t0 + j, ntok - 1) * n_head + h) * pi_pf_score_stride(n_ctx);
     };
-
-    if (w < 4) {
-#pragma unroll
-        for (uint32_t j = 0; j < TPW; j++)
-            qs[((w & 3u) * TPW + j) * DH + lane] = j < nv ? Q[(uint64_t)(t0 + j) * qdim + h * DH + lane] : 0.0f;
-    }
 
     struct Rows {
         float4 v[4];
@@ -763,6 +761,14 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
         const uint32_t p = c * kAttStep + lane;
         if (nv && p <= pos_last) {
             const float4 *kr = reinterpret_cast<const float4 *>(cur + lane * kKRow);
+            // q is the same in every lane: with a wavefront-uniform address
+            // it is read into scalar registers, leaving the LDS to K
+            const uint32_t wu = __builtin_amdgcn_readfirstlane(w & 3u);
+            const float4 *qg[TPW];
+#pragma unroll
+            for (uint32_t j = 0; j < TPW; j++)
+                qg[j] = reinterpret_cast<const float4 *>(Q + (uint64_t)min(tg * TW + wu * TPW + j, ntok - 1) * qdim +
+                                                         h * DH);
             float sc[TPW];
 #pragma unroll
             for (uint32_t j = 0; j < TPW; j++) sc[j] = 0.0f;
@@ -771,7 +777,7 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
                 const float4 kk = kr[d4];
 #pragma unroll
                 for (uint32_t j = 0; j < TPW; j++) {
-                    const float4 qq = reinterpret_cast<const float4 *>(qs + ((w & 3u) * TPW + j) * DH)[d4];
+                    const float4 qq = qg[j][d4];
                     sc[j] += qq.x * kk.x;
                     sc[j] += qq.y * kk.y;
                     sc[j] += qq.z * kk.z;
@@ -828,12 +834,14 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
             // unless v is infinite or NaN: the skip is taken only in a step
             // whose staged V holds such a value.
             bool zero = false, full = true;
+            float evs[TPW];
 #pragma unroll
             for (uint32_t j = 0; j < TPW; j++) {
                 const uint32_t pj = pos0 + t0 + j;
                 const float sv = par ? sB[j] : sA[j];
                 const bool in = j < nv && p <= pj;
                 const float ev = in ? pi_expf(sv - mx[j]) : 0.0f;
+                evs[j] = ev;
                 e0[j * kAttStep + lane] = ev;
                 zero |= __ballot(in && ev == 0.0f) != 0;
                 full &= j < nv && pj >= p0 + kAttStep - 1;
@@ -850,7 +858,11 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
                     const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
 #pragma unroll
                     for (uint32_t j = 0; j < TPW; j++) {
-                        const float4 e4 = *reinterpret_cast<const float4 *>(e0 + j * kAttStep + q);
+                        const int ei = __float_as_int(evs[j]);
+                        const float4 e4 = make_float4(__int_as_float(__builtin_amdgcn_readlane(ei, q)),
+                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 1)),
+                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 2)),
+                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 3)));
                         acc[j] = acc[j] + e4.x * v4.x;
                         acc[j] = acc[j] + e4.y * v4.y;
                         acc[j] = acc[j] + e4.z * v4.z;
