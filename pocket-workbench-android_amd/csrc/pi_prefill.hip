@@ -606,14 +606,14 @@ __global__ __launch_bounds__(256) void k_pf_swiglu_q8(const float *__restrict__ 
 // maximum is kept.
 // Pass 2, per step: the wavefront reads its tokens' scores back (loaded two
 // steps ahead), forms e_p = exp(s_p - max) lane-parallel (into an LDS step
-// buffer for wavefront 4 and the partial steps; a full step reads e_p from
-// its lane into a scalar register instead), then adds e_p * v_p[d] in
-// position order (f32_axpy order, model.rs:1056-1074: products rounded,
-// e_p == 0 skipped), lane = dimension, one chain per token, from the
-// transposed V step; lane i of wavefront 4
-// adds sum += e_p of token i in position order, one step behind.  V is
-// staged as blocks of 4 positions x 4 dimensions per thread, transposed in
-// registers, so its LDS writes are 16 bytes wide and free of bank conflicts.
+// buffer; a full step reads a quarter of its e_p from their lanes into
+// scalar registers instead), then adds e_p * v_p[d] in position order
+// (f32_axpy order, model.rs:1056-1074: products rounded, e_p == 0 skipped),
+// lane = dimension, one chain per token, from the transposed V step; lane i
+// of wavefront 4 adds sum += e_p of token i in position order, one step
+// behind.  V is staged as blocks of 4 positions x 4 dimensions per thread,
+// transposed in registers, so its LDS writes are 16 bytes wide and free of
+// bank conflicts.
 // Output acc * (1/sum), then Q8 of the head's 64 values.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kAttStep = 64;               // positions per staged step
@@ -623,6 +623,7 @@ constexpr uint32_t kAttTok = 4 * kAttTpw;       // tokens per workgroup
 constexpr uint32_t kKRow = 68;                  // floats per staged K row
 constexpr uint32_t kVRow = kAttStep + 4;        // floats per staged transposed V row
 constexpr uint32_t kAttBuf = kAttStep * kKRow;  // floats per staging buffer (>= 64 * kVRow)
+constexpr uint32_t kAttLaneE = 32;              // e of a full value step read from lanes (of TPW * 64)
 static_assert(kAttBuf >= 64 * kVRow, "staging buffer holds a transposed V step");
 static_assert(kAttTok <= 64, "wavefront 4 holds one token per lane");
 
@@ -853,16 +854,21 @@ __global__ __launch_bounds__(kAttThreads) __attribute__((amdgpu_waves_per_eu(5))
                                        vbad_at(par * 4u + 3u)) != 0u;
             const float *vr = cur + lane * kVRow;
             if (full && !skip) {
+                // e of the first kAttLaneE (token, position) pairs of the step
+                // comes from its lane (v_readlane, VALU work), the rest from
+                // the LDS step buffer (16-byte broadcast reads): the split
+                // that balances the two (measured: a quarter read from lanes
+                // ran faster than none, a half, three quarters or all)
 #pragma unroll
                 for (uint32_t q = 0; q < kAttStep; q += 4) {
                     const float4 v4 = *reinterpret_cast<const float4 *>(vr + q);
 #pragma unroll
                     for (uint32_t j = 0; j < TPW; j++) {
                         const int ei = __float_as_int(evs[j]);
-                        const float4 e4 = make_float4(__int_as_float(__builtin_amdgcn_readlane(ei, q)),
-                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 1)),
-                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 2)),
-                                                      __int_as_float(__builtin_amdgcn_readlane(ei, q + 3)));
+                        auto lane_e = [&](uint32_t i) { return __int_as_float(__builtin_amdgcn_readlane(ei, q + i)); };
+                        const float4 e4 = (j * kAttStep + q) < kAttLaneE
+                                              ? make_float4(lane_e(0), lane_e(1), lane_e(2), lane_e(3))
+                                              : *reinterpret_cast<const float4 *>(e0 + j * kAttStep + q);
                         acc[j] = acc[j] + e4.x * v4.x;
                         acc[j] = acc[j] + e4.y * v4.y;
                         acc[j] = acc[j] + e4.z * v4.z;
