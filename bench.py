@@ -26,7 +26,8 @@ Also measured here:
                 5760 x 2304 shape in Q5_K on the reference's f32 path;
   prefill    -- the 2048-token prompt on the batched int8-MFMA prefill
                 kernels (64 chunks of 32), then the prompt extended by 512
-                tokens reusing the 2048 cached positions;
+                tokens reusing the 2048 cached positions; int8_mfma gives
+                the projections' useful int8 operations over the prefill time;
   long_context -- 64 greedy tokens after 4096 and 16384 positions of N(0,1) KV;
   cpu_baseline -- the CPU oracle's int8 decode (the reference's aarch64 CPU
                 path restated) of the same model on a bounded sample, at 4
@@ -37,6 +38,7 @@ Also measured here:
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip SECTIONS]
        python bench.py --profile-gemv     (GEMV launches and a 256 MiB copy, for counter runs)
        python bench.py --profile-decode   (one config-3 decode and a 256 MiB copy, for counter runs)
+       python bench.py --profile-prefill  (the prefill workload and a 256 MiB copy, for counter runs)
 """
 import argparse
 import json
@@ -54,6 +56,7 @@ import pocketinfer_hip as pih  # noqa: E402
 
 METRIC = "decode tok/s, 2B Q4_K_M synthetic; Q4_K/Q6_K GEMV HBM GB/s (% of peak)"
 HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0   # dense int8 MFMA, MI355X
 Q4K_ROWS, Q4K_K = 5760, 2304
 Q4K_LAUNCH_BYTES = Q4K_ROWS * (Q4K_K // 256) * 144 + Q4K_K * 4 + Q4K_ROWS * 4     # 7 497 216
 Q6K_ROWS, Q6K_K = 122753, 2304
@@ -144,11 +147,22 @@ def bench_prefill(b, model, spec):
     eng.forward([ids[0]], [0], want_logits=False)   # a manual forward drops the reusable prefix
     _, sa = eng.generate(ids[:2048], 1)
     _, sb = eng.generate(ids, 1)
+    # The projections' useful int8 work: one multiply-add per layer weight per
+    # token (the int8 MFMA forms every weight x activation product once; Q6_K's
+    # half-masked operands and padded tokens are not counted).
+    qdim, kvdim = spec.n_head * spec.head_dim, spec.n_head_kv * spec.head_dim
+    macs_tok = spec.n_layer * (spec.n_embd * (qdim + 2 * kvdim) + qdim * spec.n_embd + 3 * spec.n_embd * spec.n_ff)
+    ops = 2 * macs_tok * 2048
+    tops = ops / (sa["prefill_ms"] / 1000.0) / 1e12
     return {"prompt_tokens": 2048, "prefill_ms": round(sa["prefill_ms"], 2),
             "tok_s": round(2048 / (sa["prefill_ms"] / 1000.0), 1), "chunk_tokens": 32, "pass_tokens": b.prefill_pass_tokens(),
             "extension": {"new_tokens": sb["prefill_tokens"], "reused_tokens": sb["prefill_cached_tokens"],
                           "prefill_ms": round(sb["prefill_ms"], 2),
-                          "tok_s": round(sb["prefill_tokens"] / (sb["prefill_ms"] / 1000.0), 1)}}
+                          "tok_s": round(sb["prefill_tokens"] / (sb["prefill_ms"] / 1000.0), 1)},
+            "int8_mfma": {"ops_per_prompt": ops, "tops_over_prefill": round(tops, 1), "peak_tops": INT8_PEAK_TOPS,
+                          "frac": round(tops / INT8_PEAK_TOPS, 4),
+                          "note": "useful int8 multiply-adds of the projections over the whole prefill time; "
+                                  "the exact float epilogue of each term, not the int8 dot products, bounds the GEMMs"}}
 
 
 def bench_long_context(b, model, n_fill, n_gen, wbytes):
@@ -228,6 +242,19 @@ def profile_gemv(b):
                       "copy_bytes": n}), flush=True)
 
 
+def profile_prefill(b, model, spec):
+    """The prefill workload (96-token warm-up, 2048-token prompt, 512-token
+    extension) on the per-stage kernels, then one 256 MiB device copy: a short
+    program for rocprofv3 counter runs on the prefill kernels."""
+    b.use_persistent(False)
+    st = bench_prefill(b, model, spec)
+    n = 256 << 20
+    src, dst = b.alloc(n), b.alloc(n)
+    b.copy_d2d(dst, src, n)
+    b.synchronize()
+    print(json.dumps({"profile": "prefill", "prefill_ms": st["prefill_ms"], "copy_bytes": n}), flush=True)
+
+
 def profile_decode(b, model, prompt):
     """One config-3 decode (128-id prompt, 256 tokens: k_mega at positions
     128..382) and one 256 MiB device copy: a short program for rocprofv3
@@ -281,7 +308,10 @@ def main():
                     help="engine tokens on the per-stage kernels, no cooperative launch (for profilers)")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill and long-context sections")
     ap.add_argument("--profile-gemv", action="store_true", help="GEMV launches and a device copy only")
-    ap.add_argument("--profile-decode", action="store_true", help="one 32-token decode and a device copy only")
+    ap.add_argument("--profile-decode", action="store_true",
+                    help="one config-3 decode (128-id prompt, 256 tokens) and a device copy only")
+    ap.add_argument("--profile-prefill", action="store_true",
+                    help="the prefill workload on the per-stage kernels and a device copy only")
     ap.add_argument("--no-gemv", action="store_true", help="skip the standalone GEMV measurements")
     ap.add_argument("--skip", default="", help="comma list of sections to leave out: gemv,decode,prefill,long,cpu")
     args = ap.parse_args()
@@ -341,6 +371,9 @@ def run(args, skip, steps, warmup, b, t_start):
     prompt = splitmix_ids(PROMPT_SEED, N_PROMPT, spec.n_vocab)
     if args.profile_decode:
         profile_decode(b, model, prompt)
+        return
+    if args.profile_prefill:
+        profile_prefill(b, model, spec)
         return
     runs, match, kern = [], None, []
     eng = None
