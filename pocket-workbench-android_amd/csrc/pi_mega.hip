@@ -814,11 +814,16 @@ __device__ __forceinline__ bool stage_attn(const Cfg &a, Run r, const pi_mega_la
     } else {
         const bool wlane = lane >= DHH;                          // weight lanes
         const uint32_t hr = wlane ? 0u : (lane >> 3) & 3u;       // (d / 8) & 3 of this lane's row
-        for (uint32_t c = 0; c <= nchunk; c++) {
+        // The lane's row base is fixed and the step's offset is formed with a
+        // mask, so the loop runs without divergent branches (a select
+        // between the two rows compiles to an exec-masked branch per step).
+        const float *base = wlane ? L.sc : L.hb + lane * kChunkPad;
+        const uint32_t ncu = __builtin_amdgcn_readfirstlane(nchunk);
+        const uint32_t wmask = wlane ? ~0u : 0u;
+        for (uint32_t c = 0; c <= ncu; c++) {
             if (c >= 1) {
-                const float4 *src = wlane ? reinterpret_cast<const float4 *>(L.sc + (c - 1) * kChunk)
-                                          : reinterpret_cast<const float4 *>(L.hb + ((c - 1) & 1u) * DHH * kChunkPad +
-                                                                             lane * kChunkPad);
+                const uint32_t off = ((c - 1) * kChunk & wmask) | (((c - 1) & 1u) * DHH * kChunkPad & ~wmask);
+                const float4 *src = reinterpret_cast<const float4 *>(base + off);
                 // all 16 reads of the chunk first (the scheduling barrier keeps
                 // them ahead of the adds), one LDS latency per step
                 float4 t[16];
